@@ -1,0 +1,145 @@
+/* C-ABI of the MI355X Qwen3-0.6B batch-1 decode engine (libqwen_megakernel.so).
+ *
+ * Drop-in for the launchers of the reference's Tools/megakernel/megakernel.cu,
+ * which its pybind11 layer (Tools/megakernel/qwen_ops.cpp:9-27) binds with
+ * CUDA streams. Same names, argument order and argument meaning; the stream is
+ * a hipStream_t. Plain pointers and sizes only.
+ *
+ * Buffers: every pointer is device memory owned by the caller, exactly as in
+ * the reference (Model/Qwen06B_architecture.py:205-255):
+ *   embed_weight      fp16 [151936, 1024]
+ *   layer_weights     device array of num_layers LDGLayerWeight (16-B aligned)
+ *   final_norm_weight fp16 [1024]
+ *   lm_head_weight    fp16 [151936, 1024] (tied: may equal embed_weight)
+ *   cos_table/sin_table fp16 [max_seq_len, 128]
+ *   k_cache/v_cache   fp16 [num_layers, 8, max_seq_len, 128]
+ *   hidden_buffer     fp16 [1024]   out: final-layer residual (before the final norm)
+ *   g_normalized      fp32 [1024]   out: final-normed vector fed to the lm_head
+ *   g_activations, g_residual, g_q, g_k, g_v, g_attn_out, g_mlp_intermediate,
+ *   block_max_vals, block_max_idxs: accepted for signature compatibility and
+ *   not touched; the engine keeps its inter-workgroup exchange buffers in its
+ *   own per-device workspace (allocated once, like the reference's static
+ *   barrier state, megakernel.cu:714-737).
+ *
+ * Return value: 0 on success, a QWEN_ERR_* code otherwise (the reference's
+ * launchers return void; a caller declaring them void still links and runs).
+ * Launches are asynchronous on `stream`; kernel-side failures (a wait that
+ * exceeded its deadline) are reported by qwen_last_error().
+ *
+ * One call at a time per device: all calls on a device share its workspace.
+ */
+#ifndef QWEN_MEGAKERNEL_H
+#define QWEN_MEGAKERNEL_H
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-layer weight pointers, field order of Tools/megakernel/megakernel.cu:87-100
+ * and Model/Qwen06B_architecture.py:148-160; 12 pointers (96 B), ABI version 2. */
+typedef struct __attribute__((aligned(16))) LDGLayerWeight {
+  const void* input_layernorm_weight;     /* [1024]        */
+  const void* q_proj_weight;              /* [2048, 1024]  */
+  const void* k_proj_weight;              /* [1024, 1024]  */
+  const void* v_proj_weight;              /* [1024, 1024]  */
+  const void* q_norm_weight;              /* [128]         */
+  const void* k_norm_weight;              /* [128]         */
+  const void* o_proj_weight;              /* [1024, 2048]  */
+  const void* post_attn_layernorm_weight; /* [1024]        */
+  const void* gate_proj_weight;           /* [3072, 1024]  */
+  const void* up_proj_weight;             /* [3072, 1024]  */
+  const void* down_proj_weight;           /* [1024, 3072]  */
+  const void* padding;                    /* 0             */
+} LDGLayerWeight;
+
+#define QWEN_ABI_VERSION 2
+
+#define QWEN_OK 0
+#define QWEN_ERR_ARG 1        /* bad argument (null pointer, range, alignment) */
+#define QWEN_ERR_DEVICE 2     /* not a 256-CU gfx950 device, or no cooperative launch */
+#define QWEN_ERR_LAUNCH 3     /* HIP launch/allocation failure */
+#define QWEN_ERR_TIMEOUT 4    /* a device-side wait exceeded its deadline (reported by qwen_last_error) */
+
+/* One decode step at `position` (Tools/megakernel/megakernel.cu:1150-1196):
+ * embedding of input_token_id, 28 layers writing K/V at `position`, final
+ * norm, tied lm_head, argmax -> *output_token_id (device int32). */
+int launch_ldg_decode_direct(
+    int input_token_id, int* output_token_id, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+    void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+    void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+    void* block_max_idxs, int num_layers, int position, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* Exported-but-unbound variant of the reference (megakernel.cu:1198-1244):
+ * identical to launch_ldg_decode_direct; cache_len must be position + 1. */
+int launch_ldg_decode_persistent(
+    int input_token_id, int* output_token_id, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+    void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+    void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+    void* block_max_idxs, int num_layers, int position, int cache_len,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* num_steps greedy decode steps in ONE kernel launch with no host round trip
+ * (megakernel.cu:1247-1314): step s consumes the token at position
+ * start_position + s (step 0: first_token_id, later: the previous argmax) and
+ * writes its argmax to output_log[s] (device int32[num_steps]). */
+int launch_ldg_generate_nosync(
+    int first_token_id, int num_steps, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+    void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+    void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+    void* block_max_idxs, int* output_log, int num_layers, int start_position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
+/* ---- additions (no counterpart in the reference) ---------------------------------- */
+
+/* generate_nosync with two extras, for prefill and parity checks:
+ * forced_tokens (device int32[num_steps], nullable): step s >= 1 consumes
+ *   forced_tokens[s] instead of the previous argmax (teacher forcing; a prompt
+ *   is prefilled in one launch);
+ * logits_out (device fp32[num_steps][151936], nullable): every step's logits;
+ * hidden_steps (device fp32[num_steps][1024], nullable): every step's
+ *   final-layer residual (the value written to hidden_buffer). */
+int qwen_generate_ex(
+    int first_token_id, int num_steps, const int* forced_tokens,
+    const void* embed_weight, const LDGLayerWeight* layer_weights,
+    const void* final_norm_weight, const void* lm_head_weight,
+    const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+    void* hidden_buffer, void* g_normalized, int* output_log, float* logits_out,
+    float* hidden_steps, int num_layers, int start_position, int max_seq_len,
+    float attn_scale, hipStream_t stream);
+
+/* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
+ * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
+ * Exact ties resolve to the lowest row. */
+int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token,
+                        float* logits_out, hipStream_t stream);
+
+/* Isolated MLP half-layer: y = x + down(silu(gate(n)) * up(n)), n = RMSNorm(x) * post_norm_w,
+ * with x fp16 [1024], gate/up fp16 [3072,1024], down fp16 [1024,3072], y fp32 [1024]. */
+int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, const void* gate_weight,
+                   const void* up_weight, const void* down_weight, float* y_out, hipStream_t stream);
+
+/* Synchronizes the current device and returns the device-side error state of
+ * the last launches (QWEN_OK or QWEN_ERR_TIMEOUT); clears it and resets the
+ * workspace when set. */
+int qwen_last_error(void);
+
+/* 2 (QWEN_ABI_VERSION), as qwen_ops.cpp:30-32. */
+int qwen_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_MEGAKERNEL_H */

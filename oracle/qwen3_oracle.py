@@ -145,10 +145,11 @@ class Oracle:
         self.v_cache.zero_()
 
     @torch.no_grad()
-    def step(self, token: int, pos: int) -> dict:
+    def step(self, token: int, pos: int, want_logits: bool = True) -> dict:
         """One decode step at ``pos``; writes K/V at ``pos`` and returns
         ``logits`` [V], ``hidden`` (final-layer residual before the final norm),
-        ``norm_out`` (final-normed vector) and the greedy ``token``."""
+        ``norm_out`` (final-normed vector) and the greedy ``token``. With
+        ``want_logits=False`` only the KV cache and ``hidden`` are produced."""
         s = self.shape
         assert 0 <= pos < s.max_seq
         x = self.embed[token].clone()
@@ -165,6 +166,8 @@ class Oracle:
             attn = gqa_attention(q, self.k_cache[li, :, : pos + 1], self.v_cache[li, :, : pos + 1], self.scale)
             x = x + wo @ attn.reshape(-1)
             x = x + swiglu_mlp(rms_norm(x, w_post), wg, wu, wd)
+        if not want_logits:
+            return dict(hidden=x)
         norm_out = rms_norm(x, self.final_norm)
         logits = lm_head_logits(self.embed, norm_out)
         return dict(logits=logits, hidden=x, norm_out=norm_out, token=argmax_lowest(logits))
@@ -177,7 +180,7 @@ class Oracle:
         top-2 gap and the step's outputs (logits, hidden, norm_out)."""
         pos = start
         for t in prompt[:-1]:
-            self.step(t, pos)
+            self.step(t, pos, want_logits=False)
             pos += 1
         tok = prompt[-1]
         steps = []
