@@ -138,6 +138,16 @@ int qwen_last_error(void);
 /* 2 (QWEN_ABI_VERSION), as qwen_ops.cpp:30-32. */
 int qwen_abi_version(void);
 
+/* Profiling aid: while buf is non-null, every launch on the current device
+ * records wall-clock timestamps (s_memrealtime ticks) for token index `token`
+ * of the launch into buf[workgroup][finalised stage][qwen_trace_events()]
+ * (device u64, 256 x (5*num_layers+1) x events). Events: 0 = exchange wave
+ * starts polling the stage input, 1 = input handed to the compute waves,
+ * 2 = the stage's results stored, 3 = attention merge stored / argmax known.
+ * Pass buf = NULL to stop. */
+int qwen_set_trace(unsigned long long* buf, int token);
+int qwen_trace_events(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,15 +43,15 @@ int main() {
   {
     std::vector<int> seen(QKV_ROWS, 0);
     for (int w = 0; w < NWG; ++w)
-      for (int c = 0; c < NCW; ++c)
-        for (int r = 0; r < 2; ++r) {
-          int row = QKV_PER_WG * w + 2 * c + r;
+      for (int m = 0; m < NGW; ++m)
+        for (int r = 0; r < 4; ++r) {
+          int row = QKV_PER_WG * w + 4 * m + r;
           CHECK(row < QKV_ROWS, "qkv row");
           seen[row]++;
-          int m = qkv_matrix(row), ri = qkv_row_in(row);
-          int lim = m == 0 ? QSZ : KVSZ;
+          int mat = qkv_matrix(row), ri = qkv_row_in(row);
+          int lim = mat == 0 ? QSZ : KVSZ;
           CHECK(ri >= 0 && ri < lim, "qkv row_in %d", row);
-          CHECK(m * 0 + (m == 0 ? ri : (m == 1 ? QSZ + ri : QSZ + KVSZ + ri)) == row, "qkv map %d", row);
+          CHECK((mat == 0 ? ri : (mat == 1 ? QSZ + ri : QSZ + KVSZ + ri)) == row, "qkv map %d", row);
         }
     for (int r = 0; r < QKV_ROWS; ++r) CHECK(seen[r] == 1, "qkv row %d seen %d", r, seen[r]);
     // finalize slots: slot 8w + lane holds rows 16w + 2 lane, +1
@@ -97,10 +97,10 @@ int main() {
     std::vector<int> seen(ctx, 0);
     for (int s = 0; s < NSPLIT; ++s) {
       int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s);
-      for (int c = 0; c < NCW; ++c)
+      for (int m = 0; m < NGW; ++m)
         for (int j = 0; j < 4; ++j)
-          for (int b = 0; b < 2; ++b) {
-            int lp = att_local_pos(c, j, b);
+          for (int b = 0; b < 4; ++b) {
+            int lp = att_local_pos(m, j, b);
             CHECK(lp >= 0 && lp < MAX_SPLIT_POS, "local pos");
             int p = t0 + lp;
             if (p < t1) {
@@ -154,14 +154,14 @@ int main() {
     for (int i = 0; i < QSZ; ++i) CHECK(seen[i] == 1, "combine out %d", i);
   }
 
-  // o_proj / down rows (4 per WG, row = 4w + c/2, half c&1), gate/up (12 + 12 per WG)
+  // o_proj / down rows (4 per WG, one per group member), gate/up (12 + 12 per WG, 6 per member)
   {
-    std::vector<int> oseen(HIDDEN * 2, 0), gseen(INTER, 0), useen(INTER, 0);
+    std::vector<int> oseen(HIDDEN, 0), gseen(INTER, 0), useen(INTER, 0);
     for (int w = 0; w < NWG; ++w) {
-      for (int c = 0; c < NCW; ++c) oseen[2 * (HID_PER_WG * w + (c >> 1)) + (c & 1)]++;
-      for (int c = 0; c < NCW; ++c)
-        for (int k = 0; k < 3; ++k) {
-          int lr = 3 * c + k;
+      for (int m = 0; m < NGW; ++m) oseen[HID_PER_WG * w + m]++;
+      for (int m = 0; m < NGW; ++m)
+        for (int k = 0; k < 6; ++k) {
+          int lr = 6 * m + k;
           int row = INT_PER_WG * w + (lr % INT_PER_WG);
           (lr < INT_PER_WG ? gseen : useen)[row]++;
         }
@@ -173,15 +173,13 @@ int main() {
         CHECK(in_buf(slot_int(1, (INT_PER_WG / 2) * w + lane), OFF_INT + INT_SLOTS, INT_SLOTS), "int slot");
       for (int lane = 0; lane < 2; ++lane) CHECK(in_buf(slot_arg(1, 2 * w + lane), OFF_ARG + ARG_SLOTS, ARG_SLOTS), "arg");
     }
-    for (int i = 0; i < 2 * HIDDEN; ++i) CHECK(oseen[i] == 1, "o/down half-row %d", i);
+    for (int i = 0; i < HIDDEN; ++i) CHECK(oseen[i] == 1, "o/down row %d", i);
     for (int i = 0; i < INTER; ++i) CHECK(gseen[i] == 1 && useen[i] == 1, "gate/up row %d", i);
-    // activation offsets read per lane: half*1024 + 8 lane + {0,512} < 2048 (o_proj),
-    // half*1536 + 8 lane + 512k + 8 <= 3072 (down)
-    for (int half = 0; half < 2; ++half)
-      for (int lane = 0; lane < WAVE; ++lane) {
-        CHECK(half * 1024 + 512 + 8 * lane + 8 <= QSZ, "o_proj act index");
-        for (int k = 0; k < 3; ++k) CHECK(half * 1536 + 512 * k + 8 * lane + 8 <= INTER, "down act index");
-      }
+    // activation offsets read per lane: 8 lane + 512k + 8 <= 2048 (o_proj, k < 4), <= 3072 (down, k < 6)
+    for (int lane = 0; lane < WAVE; ++lane) {
+      for (int k = 0; k < 4; ++k) CHECK(512 * k + 8 * lane + 8 <= QSZ, "o_proj act index");
+      for (int k = 0; k < 6; ++k) CHECK(512 * k + 8 * lane + 8 <= INTER, "down act index");
+    }
   }
 
   // linear polls: pair k of lane covers slots 2(lane+64k), +1 inside the buffer
@@ -213,10 +211,10 @@ int main() {
     CHECK(lm_row0(NWG - 1) + lm_rows(NWG - 1) == VOCAB, "lm rows end");
     for (int w = 0; w < NWG; ++w) {
       CHECK(lm_rows(w) <= LM_MAX_ROWS, "lm rows");
-      for (int c = 0; c < NCW; ++c)
+      for (int m = 0; m < NGW; ++m)
         for (int k = 0; k < LM_CHUNKS; ++k)
           for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i) {
-            int lr = lm_local_row(c, k, i);
+            int lr = lm_local_row(m, k, i);
             if (lr < lm_rows(w)) seen[lm_row0(w) + lr]++;
           }
     }

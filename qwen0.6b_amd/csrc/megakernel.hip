@@ -49,6 +49,9 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 constexpr float RMS_EPS = 1e-6f;
 constexpr u32 ST_TIMEOUT = 1u;
 constexpr u32 ST_BAD_TOKEN = 2u;
+// optional device timestamps (wall clock) per workgroup and finalised stage of one token
+constexpr int TRACE_EVENTS = 4;
+enum TraceEvent : int { TR_POLL = 0, TR_PUBLISH = 1, TR_FINAL = 2, TR_COMBINE = 3 };
 
 struct KParams {
   const _Float16* embed;
@@ -70,6 +73,8 @@ struct KParams {
   u64* ws;                 // exchange slots
   u32* status;             // status word (device scope)
   u64 deadline;            // wall-clock ticks a single wait may take
+  u64* trace;              // nullable [NWG][fins per token][TRACE_EVENTS]
+  int trace_token;         // token index whose stages are traced
   int mode, num_layers, first_token, start_pos, num_steps, max_seq;
   float attn_scale;
   u32 epoch0;
@@ -96,22 +101,100 @@ __device__ __forceinline__ float dot8(v4u w, const float* a) {
   return s;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+// ---- cross-lane reductions ---------------------------------------------------------
+// A wave is 4 rows of 16 lanes. Within a row: DPP row_ror (folded into v_add/v_max).
+// Across rows: gfx950 v_permlane16_swap (rows 0<->1, 2<->3) and v_permlane32_swap
+// (lanes 0-31 <-> 32-63). pack16/pack32 add two registers' partner rows and pack
+// the two results into one register, so R rows reduce in about R + 4 instructions.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int ROR8 = 0x128, ROR4 = 0x124, ROR2 = 0x122, ROR1 = 0x121;
+// every lane: sum of its 16-lane row
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<ROR8>(v);
+  v += dpp<ROR4>(v);
+  v += dpp<ROR2>(v);
+  v += dpp<ROR1>(v);
   return v;
 }
-// sum within aligned groups of 16 lanes
-__device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-  for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<ROR8>(v));
+  v = fmaxf(v, dpp<ROR4>(v));
+  v = fmaxf(v, dpp<ROR2>(v));
+  v = fmaxf(v, dpp<ROR1>(v));
   return v;
 }
-// sum within aligned groups of 32 lanes
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
+// rows of the result: 0 = a.r0 + a.r1, 1 = b.r0 + b.r1, 2 = a.r2 + a.r3, 3 = b.r2 + b.r3
+__device__ __forceinline__ float pack16(float a, float b) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// lanes 0-31 of the result: a.lo + a.hi; lanes 32-63: b.lo + b.hi
+__device__ __forceinline__ float pack32(float a, float b) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max16x(float v) {  // max of partner rows (0<->1, 2<->3)
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max32x(float v) {  // max of the two 32-lane halves
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// every lane: sum over the whole wave
+__device__ __forceinline__ float wave_sum(float v) { return row16_sum(pack16(pack32(v, v), pack32(v, v))); }
+// every lane: sum over its 32-lane half
+__device__ __forceinline__ float half_sum(float v) { return row16_sum(pack16(v, v)); }
+// every lane: sum over the 4 lanes {l, l^16, l^32, l^48} (same position in every row)
+__device__ __forceinline__ float rows4_sum(float v) {
+  const float t = pack16(v, v);
+  return pack32(t, t);
+}
+__device__ __forceinline__ float rows4_max(float v) { return max32x(max16x(v)); }
+// value of lane ^ 16 (the partner row at the same position)
+__device__ __forceinline__ float xor16(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return ((__lane_id() >> 4) & 1) ? __uint_as_float(r[0]) : __uint_as_float(r[1]);
+}
+// 4 row partials -> full sums: lanes 0-15 hold a, 16-31 c, 32-47 b, 48-63 d
+__device__ __forceinline__ float reduce4(float a, float b, float c, float d) {
+  return row16_sum(pack16(pack32(a, b), pack32(c, d)));
+}
+// 6 row partials -> full sums: p holds (a, b, d, e) and q holds (c, c, f, f) in rows 0..3
+__device__ __forceinline__ void reduce6(const float (&v)[6], float& p, float& q) {
+  const float x1 = pack32(v[0], v[3]), x2 = pack32(v[1], v[4]), x3 = pack32(v[2], v[5]);
+  p = row16_sum(pack16(x1, x2));
+  q = row16_sum(pack16(x3, x3));
+}
+// (value, index) arg-max over the whole wave, lowest index on ties; every lane gets the result
+__device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  better(v, i, dpp<ROR8>(v), dpp_i<ROR8>(i));
+  better(v, i, dpp<ROR4>(v), dpp_i<ROR4>(i));
+  better(v, i, dpp<ROR2>(v), dpp_i<ROR2>(i));
+  better(v, i, dpp<ROR1>(v), dpp_i<ROR1>(i));
+  auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  auto ri = __builtin_amdgcn_permlane16_swap((unsigned)i, (unsigned)i, false, false);
+  v = __uint_as_float(rv[0]);
+  i = (int)ri[0];
+  better(v, i, __uint_as_float(rv[1]), (int)ri[1]);
+  rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  ri = __builtin_amdgcn_permlane32_swap((unsigned)i, (unsigned)i, false, false);
+  v = __uint_as_float(rv[0]);
+  i = (int)ri[0];
+  better(v, i, __uint_as_float(rv[1]), (int)ri[1]);
 }
 
 __device__ __forceinline__ u32 pack_h2(float a, float b) {
@@ -152,7 +235,8 @@ struct Shared {
   float xres[HID_PER_WG];        // residual rows before attention (fp32)
   float actres[HID_PER_WG];      // residual rows after attention (fp32)
   u32 ready;                     // fin + 1 of the newest prepared input
-  u32 cnt[2];                    // compute-wave arrivals per fin parity
+  u32 cnt[2];                    // compute-wave arrivals at the current fin of each parity
+  u32 done[2];                   // fin + 1 of the newest finalised fin of each parity
   u32 abort;
 };
 
@@ -167,14 +251,22 @@ struct Poll {
 };
 
 __device__ __forceinline__ bool poll_give_up(Poll& pl, u64 t0, int& spins) {
-  if (wall_clock64() - t0 > pl.P->deadline) {
+  ++spins;
+  if ((spins & 15) == 0 && wall_clock64() - t0 > pl.P->deadline) {
     __hip_atomic_fetch_or(pl.P->status, ST_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
   }
-  if ((++spins & 255) == 0) {
+  if ((spins & 255) == 0) {
     if (__hip_atomic_load(pl.P->status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return true;
   }
   return false;
+}
+
+__device__ __forceinline__ void xtrace(const KParams& P, int token, u32 fin_in_token, int what) {
+  if (P.trace && token == P.trace_token && __lane_id() == 0) {
+    const int FT = fins_per_token(P.mode, P.num_layers);
+    P.trace[((long)blockIdx.x * FT + fin_in_token) * TRACE_EVENTS + what] = wall_clock64();
+  }
 }
 
 // Polls K slot pairs per lane until both slots of every pair carry `tag`. Pair k
@@ -211,13 +303,12 @@ __device__ __forceinline__ void poll_pairs(Poll& pl, u32 tag, int voff, bool act
   }
 }
 
-// exchange wave: wait until the compute waves finished reading in[fin % 2] of fin-2
+// exchange wave: wait until fin - 2 (same parity) is finalised, so in[fin % 2] is free
 __device__ __forceinline__ void wait_consumed(Poll& pl, u32 fin) {
   if (!pl.ok || fin < 2) return;
-  const u32 need = NCW * (fin / 2);
   const u64 t0 = wall_clock64();
   int spins = 0;
-  while (lds_ld(&pl.S->cnt[fin & 1]) < need) {
+  while (lds_ld(&pl.S->done[fin & 1]) < fin - 1) {
     if (poll_give_up(pl, t0, spins)) {
       pl.ok = false;
       return;
@@ -255,15 +346,26 @@ __device__ __forceinline__ void poll_vec1024(Poll& pl, u32 tag, long base, float
   }
 }
 
+// the lane's 16 norm weights w[4(lane + 64k) + j]; loaded before polling so the
+// load overlaps the wait instead of following it
+struct NormW {
+  h4 v[4];
+};
+__device__ __forceinline__ NormW load_norm(const _Float16* w) {
+  NormW n;
+  const int lane = __lane_id();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) n.v[k] = *(const h4*)(w + 4 * (lane + 64 * k));
+  return n;
+}
 // in[i] = x[i] * rstd * w[i] for the lane's 16 values
-__device__ __forceinline__ void store_normed(float* dst, const float (&x)[16], float rstd, const _Float16* w) {
+__device__ __forceinline__ void store_normed(float* dst, const float (&x)[16], float rstd, const NormW& wv) {
   const int lane = __lane_id();
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int i = 4 * (lane + 64 * k);
-    h4 wv = *(const h4*)(w + i);
-    float4 o = make_float4(x[4 * k] * rstd * (float)wv[0], x[4 * k + 1] * rstd * (float)wv[1],
-                           x[4 * k + 2] * rstd * (float)wv[2], x[4 * k + 3] * rstd * (float)wv[3]);
+    float4 o = make_float4(x[4 * k] * rstd * (float)wv.v[k][0], x[4 * k + 1] * rstd * (float)wv.v[k][1],
+                           x[4 * k + 2] * rstd * (float)wv.v[k][2], x[4 * k + 3] * rstd * (float)wv.v[k][3]);
     *(float4*)(dst + i) = o;
   }
 }
@@ -288,7 +390,7 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
       for (int j = 0; j < 4; ++j) x[4 * k + j] = (float)v[j];
     }
     const float rs = rstd_1024(x);
-    store_normed(S->in[0], x, rs, (const _Float16*)lw.post_attn_layernorm_weight);
+    store_normed(S->in[0], x, rs, load_norm((const _Float16*)lw.post_attn_layernorm_weight));
     if (lane < HID_PER_WG) S->actres[lane] = (float)P.in_vec[HID_PER_WG * w + lane];
     publish(pl, 0);
     // DOWN input: SiLU(gate)*up from every workgroup
@@ -331,6 +433,8 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
         u32 fin = (u32)(t * FT + 5 * l);
         // ---- QKV input: residual stream -> RMSNorm * input_layernorm
         wait_consumed(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
+        const NormW w_in = load_norm((const _Float16*)lw.input_layernorm_weight);
         float x[16];
         if (l == 0) {
           const _Float16* row = P.embed + (long)token * HIDDEN;
@@ -346,15 +450,22 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
         if (!pl.ok) break;
         {
           const float rs = rstd_1024(x);
-          store_normed(S->in[fin & 1], x, rs, (const _Float16*)lw.input_layernorm_weight);
+          store_normed(S->in[fin & 1], x, rs, w_in);
         }
         publish(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
 
         // ---- attention input: raw q (2 heads), k, v of kv head g -> norms, RoPE, KV write
         ++fin;
         wait_consumed(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
         const int g = att_kv(w), s = att_split(w);
         {
+          const int d0 = 4 * (lane & 31);
+          const h4 cv = *(const h4*)(P.cos_t + (long)pos * HD + d0);
+          const h4 sv = *(const h4*)(P.sin_t + (long)pos * HD + d0);
+          const h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d0);
+          const h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d0);
           v4u v[2];
           // pair k = 0: q slots 128g + 2 lane; k = 1: k slots (lane < 32) or v slots (lane >= 32)
           poll_pairs<1>(pl, tag_of(epoch, l, SID_QKV), attq_voff(lane), true,
@@ -366,13 +477,6 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           // k = 1: lane < 32: k dims 4 lane.., lane >= 32: v dims 4(lane-32)..
           float q[4] = {lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z)};
           float kv[4] = {lo_h(v[1].x), hi_h(v[1].x), lo_h(v[1].z), hi_h(v[1].z)};
-          const int d0 = 4 * (lane & 31);
-          const _Float16* cs = P.cos_t + (long)pos * HD;
-          const _Float16* sn = P.sin_t + (long)pos * HD;
-          h4 cv = *(const h4*)(cs + d0);
-          h4 sv = *(const h4*)(sn + d0);
-          h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d0);
-          h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d0);
           // q head norms (each 32-lane half is one head)
           float ssq = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
           ssq = half_sum(ssq);
@@ -391,8 +495,8 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           float qo[4], ko[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float qp = __shfl_xor(qq[j], 16);
-            const float kp = __shfl_xor(kk[j], 16);
+            const float qp = xor16(qq[j]);
+            const float kp = xor16(kk[j]);
             const float c = (float)cv[j], sgn = lo_half ? -(float)sv[j] : (float)sv[j];
             qo[j] = qq[j] * c + qp * sgn;
             ko[j] = kk[j] * c + kp * sgn;
@@ -418,6 +522,7 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           }
         }
         publish(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
 
         // ---- combine: q head w/16, dims [d0, d0+8) over the 32 splits of its kv head
         {
@@ -437,9 +542,7 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
               acc[2 * k + 1] = __uint_as_float(v[k + 1].z);
             }
           }
-          float M = m;
-#pragma unroll
-          for (int msk = 16; msk >= 1; msk >>= 1) M = fmaxf(M, __shfl_xor(M, msk));
+          const float M = max16x(row16_max(m));  // over lanes 0-31 (lanes >= 32 hold -inf)
           const float e = (lane < NSPLIT && m != -INFINITY) ? __expf(m - M) : 0.f;
           float Lt = half_sum(e * lsum);
           float o[8];
@@ -451,11 +554,13 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           if (lane < 4)
             ll_store(P.ws, slot_att(par, 4 * w + lane), pack_h2(o[2 * lane] * inv, o[2 * lane + 1] * inv),
                      tag_of(epoch, l, SID_ATT));
+          xtrace(P, t, fin - (u32)(t * FT), TR_COMBINE);
         }
 
         // ---- o_proj input: all 2048 attention values
         ++fin;
         wait_consumed(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
         {
           v4u v[8];
           poll_pairs<8>(pl, tag_of(epoch, l, SID_ATT), lin_voff(lane), true,
@@ -467,21 +572,26 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
             *(float4*)(in + 4 * (lane + 64 * k)) = make_float4(lo_h(v[k].x), hi_h(v[k].x), lo_h(v[k].z), hi_h(v[k].z));
         }
         publish(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
 
         // ---- gate/up input: post-attention residual -> RMSNorm * post_attention_layernorm
         ++fin;
         wait_consumed(pl, fin);
-        poll_vec1024(pl, tag_of(epoch, l, SID_ACT), slot_act(par, 0), x);
-        if (!pl.ok) break;
+        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
         {
+          const NormW w_post = load_norm((const _Float16*)lw.post_attn_layernorm_weight);
+          poll_vec1024(pl, tag_of(epoch, l, SID_ACT), slot_act(par, 0), x);
+          if (!pl.ok) break;
           const float rs = rstd_1024(x);
-          store_normed(S->in[fin & 1], x, rs, (const _Float16*)lw.post_attn_layernorm_weight);
+          store_normed(S->in[fin & 1], x, rs, w_post);
         }
         publish(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
 
         // ---- down input: SiLU(gate)*up, 3072 values
         ++fin;
         wait_consumed(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
         {
           v4u v[12];
           poll_pairs<12>(pl, tag_of(epoch, l, SID_INT), lin_voff(lane), true,
@@ -493,25 +603,29 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
             *(float4*)(in + 4 * (lane + 64 * k)) = make_float4(lo_h(v[k].x), hi_h(v[k].x), lo_h(v[k].z), hi_h(v[k].z));
         }
         publish(pl, fin);
+        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
       }
       if (!pl.ok) break;
 
       // ---- lm_head input: final residual -> RMSNorm * final_norm
       const u32 fin = (u32)(t * FT + 5 * L);
       wait_consumed(pl, fin);
+      xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
+      const NormW w_fin = load_norm(P.final_norm);
       float x[16];
       poll_vec1024(pl, tag_of(epoch, L - 1, SID_X), slot_x(L & 1, 0), x);
       if (!pl.ok) break;
       const float rs = rstd_1024(x);
-      store_normed(S->in[fin & 1], x, rs, P.final_norm);
+      store_normed(S->in[fin & 1], x, rs, w_fin);
       publish(pl, fin);
+      xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
       if (w == 0) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const int i = 4 * (lane + 64 * k);
           h4 hv = {(_Float16)x[4 * k], (_Float16)x[4 * k + 1], (_Float16)x[4 * k + 2], (_Float16)x[4 * k + 3]};
           *(h4*)(P.hidden_out + i) = hv;
-          h4 wv = *(const h4*)(P.final_norm + i);
+          const h4 wv = w_fin.v[k];
           *(float4*)(P.norm_out + i) = make_float4(x[4 * k] * rs * (float)wv[0], x[4 * k + 1] * rs * (float)wv[1],
                                                    x[4 * k + 2] * rs * (float)wv[2], x[4 * k + 3] * rs * (float)wv[3]);
           if (P.hidden_steps)
@@ -537,17 +651,10 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           bidx = idx;
         }
       }
-#pragma unroll
-      for (int msk = 32; msk >= 1; msk >>= 1) {
-        const float ov = __shfl_xor(best, msk);
-        const int oi = __shfl_xor(bidx, msk);
-        if (ov > best || (ov == best && oi < bidx)) {
-          best = ov;
-          bidx = oi;
-        }
-      }
+      wave_argmax(best, bidx);
       if (bidx < 0 || bidx >= VOCAB) bidx = 0;  // every logit NaN
       if (w == 0 && lane == 0) P.out_tokens[t] = bidx;
+      xtrace(P, t, (u32)(FT - 1), TR_COMBINE);
       token = (P.forced && t + 1 < P.num_steps) ? P.forced[t + 1] : bidx;
       if (token < 0 || token >= VOCAB) {  // a forced id out of range: report and stop
         __hip_atomic_fetch_or(P.status, ST_BAD_TOKEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -563,21 +670,24 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
 // compute waves
 
 struct Buf {
-  v4u v[6];
+  v4u v[12];
 };
 
 __device__ __forceinline__ const LDGLayerWeight& layer_of(const KParams& P, int l) { return P.layers[l]; }
 
-__device__ __forceinline__ void prefetch(const KParams& P, const StageDesc& d, Buf& b, int w, int c, int lane) {
+// Issues stage d's weight (or KV-cache) loads for group member m into b. Every
+// path issues its loads unconditionally; rows outside the work range are
+// clamped to a valid row and ignored by the compute.
+__device__ __forceinline__ void prefetch(const KParams& P, const StageDesc& d, Buf& b, int w, int m, int lane) {
   switch (d.type) {
     case C_QKV: {
       const LDGLayerWeight& lw = layer_of(P, d.layer);
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int row = QKV_PER_WG * w + 2 * c + r;
-        const int m = qkv_matrix(row);
+      for (int r = 0; r < 4; ++r) {
+        const int row = QKV_PER_WG * w + 4 * m + r;
+        const int mat = qkv_matrix(row);
         const _Float16* base =
-            (const _Float16*)(m == 0 ? lw.q_proj_weight : (m == 1 ? lw.k_proj_weight : lw.v_proj_weight)) +
+            (const _Float16*)(mat == 0 ? lw.q_proj_weight : (mat == 1 ? lw.k_proj_weight : lw.v_proj_weight)) +
             (long)qkv_row_in(row) * HIDDEN;
         b.v[2 * r] = ld_nt(base + 8 * lane);
         b.v[2 * r + 1] = ld_nt(base + 512 + 8 * lane);
@@ -590,34 +700,29 @@ __device__ __forceinline__ void prefetch(const KParams& P, const StageDesc& d, B
       const int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s);
       const int j = lane >> 4, q = lane & 15;
 #pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int p = t0 + att_local_pos(c, j, bb);
-        if (p < t1 && p != pos) {
-          const long row = (((long)d.layer * NKV + g) * P.max_seq + p) * HD + 8 * q;
-          b.v[bb] = ld_plain(P.k_cache + row);
-          b.v[2 + bb] = ld_plain(P.v_cache + row);
-        } else {
-          b.v[bb] = v4u{0, 0, 0, 0};
-          b.v[2 + bb] = v4u{0, 0, 0, 0};
-        }
+      for (int bb = 0; bb < 4; ++bb) {
+        int p = t0 + att_local_pos(m, j, bb);
+        if (!(p < t1 && p != pos)) p = 0;  // position 0 always exists; its value is unused
+        const long row = (((long)d.layer * NKV + g) * P.max_seq + p) * HD + 8 * q;
+        b.v[bb] = ld_plain(P.k_cache + row);
+        b.v[4 + bb] = ld_plain(P.v_cache + row);
       }
       break;
     }
     case C_OPROJ: {
       const LDGLayerWeight& lw = layer_of(P, d.layer);
-      const int row = HID_PER_WG * w + (c >> 1), half = c & 1;
-      const _Float16* base = (const _Float16*)lw.o_proj_weight + (long)row * QSZ + half * 1024;
-      b.v[0] = ld_nt(base + 8 * lane);
-      b.v[1] = ld_nt(base + 512 + 8 * lane);
+      const _Float16* base = (const _Float16*)lw.o_proj_weight + (long)(HID_PER_WG * w + m) * QSZ;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) b.v[k] = ld_nt(base + 8 * lane + 512 * k);
       break;
     }
     case C_GU: {
       const LDGLayerWeight& lw = layer_of(P, d.layer);
+      // member 0,1: gate rows 6m..6m+5; member 2,3: up rows 6(m-2)..
+      const _Float16* mat = (const _Float16*)(m < 2 ? lw.gate_proj_weight : lw.up_proj_weight);
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const int lr = 3 * c + k;  // 0..23: gate rows 0..11, up rows 12..23
-        const _Float16* mat = (const _Float16*)(lr < INT_PER_WG ? lw.gate_proj_weight : lw.up_proj_weight);
-        const _Float16* base = mat + (long)(INT_PER_WG * w + (lr % INT_PER_WG)) * HIDDEN;
+      for (int k = 0; k < 6; ++k) {
+        const _Float16* base = mat + (long)(INT_PER_WG * w + 6 * (m & 1) + k) * HIDDEN;
         b.v[2 * k] = ld_nt(base + 8 * lane);
         b.v[2 * k + 1] = ld_nt(base + 512 + 8 * lane);
       }
@@ -625,25 +730,20 @@ __device__ __forceinline__ void prefetch(const KParams& P, const StageDesc& d, B
     }
     case C_DOWN: {
       const LDGLayerWeight& lw = layer_of(P, d.layer);
-      const int row = HID_PER_WG * w + (c >> 1), half = c & 1;
-      const _Float16* base = (const _Float16*)lw.down_proj_weight + (long)row * INTER + half * 1536;
+      const _Float16* base = (const _Float16*)lw.down_proj_weight + (long)(HID_PER_WG * w + m) * INTER;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) b.v[k] = ld_nt(base + 8 * lane + 512 * k);
+      for (int k = 0; k < 6; ++k) b.v[k] = ld_nt(base + 8 * lane + 512 * k);
       break;
     }
     default: {  // C_LMH
       const int nrows = lm_rows(w), r0 = lm_row0(w);
 #pragma unroll
       for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i) {
-        const int lr = lm_local_row(c, d.chunk, i);
-        if (lr < nrows) {
-          const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
-          b.v[2 * i] = ld_nt(base + 8 * lane);
-          b.v[2 * i + 1] = ld_nt(base + 512 + 8 * lane);
-        } else {
-          b.v[2 * i] = v4u{0, 0, 0, 0};
-          b.v[2 * i + 1] = v4u{0, 0, 0, 0};
-        }
+        int lr = lm_local_row(m, d.chunk, i);
+        if (lr >= nrows) lr = nrows - 1;  // clamped rows are loaded but not used
+        const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
+        b.v[2 * i] = ld_nt(base + 8 * lane);
+        b.v[2 * i + 1] = ld_nt(base + 512 + 8 * lane);
       }
       break;
     }
@@ -662,45 +762,71 @@ __device__ __forceinline__ bool wait_ready(Shared* S, u32 fin, u64 deadline) {
     return true;
   }
   const u64 t0 = wall_clock64();
+  int spins = 0;
   while (lds_ld(&S->ready) <= fin) {
     if (lds_ld(&S->abort)) return false;
-    if (wall_clock64() - t0 > deadline) return false;
-    __builtin_amdgcn_s_sleep(2);
+    if ((++spins & 63) == 0 && wall_clock64() - t0 > deadline) return false;
+    __builtin_amdgcn_s_sleep(1);
   }
   lds_acquire();
   return true;
 }
 
-// one compute wave's arrival; returns true in the wave that arrives last (it finalises)
-__device__ __forceinline__ bool arrive(Shared* S, u32 fin) {
+// One compute wave's arrival at finalised stage `fin`, which takes `n` arrivals;
+// returns true in the wave that arrives last: it finalises (and resets the counter).
+__device__ __forceinline__ bool arrive(Shared* S, u32 fin, u32 n) {
   lds_release();
   u32 old = 0;
   if (__lane_id() == 0) old = __hip_atomic_fetch_add(&S->cnt[fin & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  old = __shfl(old, 0);
-  const bool last = (old % NCW) == NCW - 1;
-  if (last) lds_acquire();
+  old = __builtin_amdgcn_readfirstlane(old);
+  const bool last = old == n - 1;
+  if (last) {
+    lds_acquire();
+    if (__lane_id() == 0) lds_st(&S->cnt[fin & 1], 0u);
+  }
   return last;
 }
 
+// marks `fin` finalised (all its reads of S->in and S->red are done) for the exchange wave;
+// called by the finalising wave after its last LDS read and before its exchange stores
+__device__ __forceinline__ void mark_done(Shared* S, u32 fin) {
+  lds_release();
+  if (__lane_id() == 0) lds_st(&S->done[fin & 1], fin + 1);
+}
+
+__device__ __forceinline__ void trace_mark(const KParams& P, int token, u32 fin_in_token, int what) {
+  if (P.trace && token == P.trace_token && __lane_id() == 0) {
+    const int FT = fins_per_token(P.mode, P.num_layers);
+    P.trace[((long)blockIdx.x * FT + fin_in_token) * TRACE_EVENTS + what] = wall_clock64();
+  }
+}
+
 __device__ __forceinline__ void compute(const KParams& P, Shared* S, const StageDesc& d, const Buf& b, CState& cs,
-                                        int w, int c, int lane) {
+                                        int w, int m, int c, int lane) {
   const u32 fin = (u32)d.fin;
   const float* in = S->in[fin & 1];
   float* red = S->red[fin & 1];
   const u32 epoch = P.epoch0 + (u32)d.token;
   const int par = d.layer & 1;
+  const u32 fin_in_token = fin - (u32)(d.token * fins_per_token(P.mode, P.num_layers));
   switch (d.type) {
     case C_QKV: {
+      float part[4];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        float s = dot8(b.v[2 * r], in + 8 * lane) + dot8(b.v[2 * r + 1], in + 512 + 8 * lane);
-        s = wave_sum(s);
-        if (lane == 0) red[2 * c + r] = s;
-      }
-      if (arrive(S, fin)) {
+      for (int r = 0; r < 4; ++r) part[r] = dot8(b.v[2 * r], in + 8 * lane) + dot8(b.v[2 * r + 1], in + 512 + 8 * lane);
+      // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
+      const float rs = reduce4(part[0], part[1], part[2], part[3]);
+      if ((lane & 15) == 0) red[4 * m + ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : (lane >> 4)))] = rs;
+      if (arrive(S, fin, NGW)) {
+        float v0 = 0.f, v1 = 0.f;
+        if (lane < QKV_PER_WG / 2) {
+          v0 = red[2 * lane];
+          v1 = red[2 * lane + 1];
+        }
+        mark_done(S, fin);
         if (lane < QKV_PER_WG / 2)
-          ll_store(P.ws, slot_qkv(par, (QKV_PER_WG / 2) * w + lane), pack_h2(red[2 * lane], red[2 * lane + 1]),
-                   tag_of(epoch, d.layer, SID_QKV));
+          ll_store(P.ws, slot_qkv(par, (QKV_PER_WG / 2) * w + lane), pack_h2(v0, v1), tag_of(epoch, d.layer, SID_QKV));
+        trace_mark(P, d.token, fin_in_token, TR_FINAL);
       }
       break;
     }
@@ -713,62 +839,74 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
       const float* q1 = in + 128;
       const float* kr = in + 256;
       const float* vr = in + 384;
-      float sc[2][2];
-      float vv[2][8];
-      bool valid[2];
+      float4 qa0 = *(const float4*)(q0 + 8 * q), qb0 = *(const float4*)(q0 + 8 * q + 4);
+      float4 qa1 = *(const float4*)(q1 + 8 * q), qb1 = *(const float4*)(q1 + 8 * q + 4);
+      const float qv0[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qb0.x, qb0.y, qb0.z, qb0.w};
+      const float qv1[8] = {qa1.x, qa1.y, qa1.z, qa1.w, qb1.x, qb1.y, qb1.z, qb1.w};
+      float sc[4][2];
+      bool valid[4];
 #pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int p = t0 + att_local_pos(c, j, bb);
+      for (int bb = 0; bb < 4; ++bb) {
+        const int p = t0 + att_local_pos(m, j, bb);
         valid[bb] = p < t1;
         float kf[8];
         if (p == pos) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kf[e] = (float)(_Float16)kr[8 * q + e];  // the cached value is fp16
-            vv[bb][e] = (float)(_Float16)vr[8 * q + e];
-          }
+          for (int e = 0; e < 8; ++e) kf[e] = (float)(_Float16)kr[8 * q + e];  // the cached value is fp16
         } else {
           h8 kh = __builtin_bit_cast(h8, b.v[bb]);
-          h8 vh = __builtin_bit_cast(h8, b.v[2 + bb]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kf[e] = (float)kh[e];
-            vv[bb][e] = (float)vh[e];
-          }
+          for (int e = 0; e < 8; ++e) kf[e] = (float)kh[e];
         }
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          s0 = fmaf(kf[e], q0[8 * q + e], s0);
-          s1 = fmaf(kf[e], q1[8 * q + e], s1);
+          s0 = fmaf(kf[e], qv0[e], s0);
+          s1 = fmaf(kf[e], qv1[e], s1);
         }
-        s0 = group16_sum(s0) * P.attn_scale;
-        s1 = group16_sum(s1) * P.attn_scale;
+        s0 = row16_sum(s0) * P.attn_scale;
+        s1 = row16_sum(s1) * P.attn_scale;
         sc[bb][0] = valid[bb] ? s0 : -INFINITY;
         sc[bb][1] = valid[bb] ? s1 : -INFINITY;
       }
       float mh[2], lh[2], acc[2][8];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        float m = fmaxf(sc[0][h], sc[1][h]);
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-        mh[h] = m;
-        const float p0 = valid[0] ? __expf(sc[0][h] - m) : 0.f;
-        const float p1 = valid[1] ? __expf(sc[1][h] - m) : 0.f;
-        float l = p0 + p1;
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
+        float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
+        mx = rows4_max(mx);
+        mh[h] = mx;
+        float pr[4];
+        float l = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          pr[bb] = valid[bb] ? __expf(sc[bb][h] - mx) : 0.f;
+          l += pr[bb];
+        }
+        l = rows4_sum(l);
         lh[h] = l;
 #pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < 4; ++bb) {
+          const int p = t0 + att_local_pos(m, j, bb);
+          float vf[8];
+          if (p == pos) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vf[e] = (float)(_Float16)vr[8 * q + e];
+          } else {
+            h8 vh = __builtin_bit_cast(h8, b.v[4 + bb]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vf[e] = (float)vh[e];
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pr[bb], vf[e], acc[h][e]);
+        }
+#pragma unroll
         for (int e = 0; e < 8; ++e) {
-          float a = p0 * vv[0][e] + p1 * vv[1][e];
-          a += __shfl_xor(a, 16);
-          a += __shfl_xor(a, 32);
-          acc[h][e] = a;
+          acc[h][e] = rows4_sum(acc[h][e]);
         }
       }
-      float* rec = red + c * 260;
+      float* rec = red + m * 260;
       if (lane < 16) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -782,143 +920,188 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
         rec[130] = mh[1];
         rec[131] = lh[1];
       }
-      if (arrive(S, fin)) {
-        // merge the 8 wave partials into the workgroup partial (m, l, acc) per head
-        float Mx[2], wt[2][NCW];
+      if (arrive(S, fin, NGW)) {
+        // merge the 4 wave partials into the workgroup partial (m, l, acc) per head
+        float Mx[2], wt[2][NGW];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float M = -INFINITY;
 #pragma unroll
-          for (int cc = 0; cc < NCW; ++cc) M = fmaxf(M, red[cc * 260 + h * 130]);
+          for (int cc = 0; cc < NGW; ++cc) M = fmaxf(M, red[cc * 260 + h * 130]);
           Mx[h] = M;
 #pragma unroll
-          for (int cc = 0; cc < NCW; ++cc) {
+          for (int cc = 0; cc < NGW; ++cc) {
             const float mc = red[cc * 260 + h * 130];
             wt[h][cc] = (mc == -INFINITY) ? 0.f : __expf(mc - M);
           }
         }
+        float vals[5];
+#pragma unroll
+        for (int it = 0; it < 5; ++it) {
+          const int e = lane + 64 * it;
+          vals[it] = 0.f;
+          if (e < 260) {
+            const bool h1 = e >= 130;
+            const int k = h1 ? e - 130 : e;
+            if (k == 0) {
+              vals[it] = h1 ? Mx[1] : Mx[0];
+            } else {
+#pragma unroll
+              for (int cc = 0; cc < NGW; ++cc)
+                vals[it] = fmaf(h1 ? wt[1][cc] : wt[0][cc], red[cc * 260 + e], vals[it]);
+            }
+          }
+        }
+        mark_done(S, fin);
 #pragma unroll
         for (int it = 0; it < 5; ++it) {
           const int e = lane + 64 * it;
           if (e < 260) {
             const bool h1 = e >= 130;
-            const int k = h1 ? e - 130 : e;
-            float val;
-            if (k == 0) {
-              val = h1 ? Mx[1] : Mx[0];
-            } else {
-              val = 0.f;
-#pragma unroll
-              for (int cc = 0; cc < NCW; ++cc) val = fmaf(h1 ? wt[1][cc] : wt[0][cc], red[cc * 260 + e], val);
-            }
-            ll_store(P.ws, slot_part(par, g, s, h1 ? 1 : 0, k), __float_as_uint(val), tag_of(epoch, d.layer, SID_PART));
+            ll_store(P.ws, slot_part(par, g, s, h1 ? 1 : 0, h1 ? e - 130 : e), __float_as_uint(vals[it]),
+                     tag_of(epoch, d.layer, SID_PART));
           }
         }
+        trace_mark(P, d.token, fin_in_token, TR_FINAL);
       }
       break;
     }
     case C_OPROJ: {
-      const int half = c & 1;
-      float sum = dot8(b.v[0], in + half * 1024 + 8 * lane) + dot8(b.v[1], in + half * 1024 + 512 + 8 * lane);
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sum += dot8(b.v[k], in + 8 * lane + 512 * k);
       sum = wave_sum(sum);
-      if (lane == 0) red[c] = sum;
-      if (arrive(S, fin)) {
+      if (lane == 0) red[m] = sum;
+      if (arrive(S, fin, NGW)) {
+        float a0 = 0.f, a1 = 0.f;
         if (lane < 2) {
           const int r0 = 2 * lane;
-          const float a0 = red[2 * r0] + red[2 * r0 + 1] + S->xres[r0];
-          const float a1 = red[2 * r0 + 2] + red[2 * r0 + 3] + S->xres[r0 + 1];
+          a0 = red[r0] + S->xres[r0];
+          a1 = red[r0 + 1] + S->xres[r0 + 1];
           S->actres[r0] = a0;
           S->actres[r0 + 1] = a1;
-          ll_store(P.ws, slot_act(par, 2 * w + lane), pack_h2(a0, a1), tag_of(epoch, d.layer, SID_ACT));
         }
+        mark_done(S, fin);
+        if (lane < 2) ll_store(P.ws, slot_act(par, 2 * w + lane), pack_h2(a0, a1), tag_of(epoch, d.layer, SID_ACT));
+        trace_mark(P, d.token, fin_in_token, TR_FINAL);
       }
       break;
     }
     case C_GU: {
+      float part[6];
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        float sum = dot8(b.v[2 * k], in + 8 * lane) + dot8(b.v[2 * k + 1], in + 512 + 8 * lane);
-        sum = wave_sum(sum);
-        if (lane == 0) red[3 * c + k] = sum;
-      }
-      if (arrive(S, fin)) {
+      for (int k = 0; k < 6; ++k) part[k] = dot8(b.v[2 * k], in + 8 * lane) + dot8(b.v[2 * k + 1], in + 512 + 8 * lane);
+      float pr, qr;
+      reduce6(part, pr, qr);  // pr: rows 0,1,3,4 at lanes 0,16,32,48; qr: rows 2 (lane 0), 5 (lane 32)
+      if ((lane & 15) == 0) red[6 * m + (lane >> 4) + ((lane >> 4) >= 2 ? 1 : 0)] = pr;
+      if ((lane & 31) == 0) red[6 * m + (lane == 0 ? 2 : 5)] = qr;
+      if (arrive(S, fin, NGW)) {
+        float o[2] = {0.f, 0.f};
         if (lane < INT_PER_WG / 2) {
-          float o[2];
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
             const float gt = red[2 * lane + e], up = red[INT_PER_WG + 2 * lane + e];
             o[e] = gt / (1.0f + __expf(-gt)) * up;
           }
-          ll_store(P.ws, slot_int(par, (INT_PER_WG / 2) * w + lane), pack_h2(o[0], o[1]), tag_of(epoch, d.layer, SID_INT));
         }
+        mark_done(S, fin);
+        if (lane < INT_PER_WG / 2)
+          ll_store(P.ws, slot_int(par, (INT_PER_WG / 2) * w + lane), pack_h2(o[0], o[1]), tag_of(epoch, d.layer, SID_INT));
+        trace_mark(P, d.token, fin_in_token, TR_FINAL);
       }
       break;
     }
     case C_DOWN: {
-      const int half = c & 1;
       float sum = 0.f;
 #pragma unroll
-      for (int k = 0; k < 3; ++k) sum += dot8(b.v[k], in + half * 1536 + 8 * lane + 512 * k);
+      for (int k = 0; k < 6; ++k) sum += dot8(b.v[k], in + 8 * lane + 512 * k);
       sum = wave_sum(sum);
-      if (lane == 0) red[c] = sum;
-      if (arrive(S, fin)) {
+      if (lane == 0) red[m] = sum;
+      if (arrive(S, fin, NGW)) {
+        float x0 = 0.f, x1 = 0.f;
         if (lane < 2) {
           const int r0 = 2 * lane;
-          const float x0 = red[2 * r0] + red[2 * r0 + 1] + S->actres[r0];
-          const float x1 = red[2 * r0 + 2] + red[2 * r0 + 3] + S->actres[r0 + 1];
+          x0 = red[r0] + S->actres[r0];
+          x1 = red[r0 + 1] + S->actres[r0 + 1];
           S->xres[r0] = x0;
           S->xres[r0 + 1] = x1;
+        }
+        mark_done(S, fin);
+        if (lane < 2) {
           if (P.mode == MODE_MLP) {
-            P.out_vec[HID_PER_WG * w + r0] = x0;
-            P.out_vec[HID_PER_WG * w + r0 + 1] = x1;
+            P.out_vec[HID_PER_WG * w + 2 * lane] = x0;
+            P.out_vec[HID_PER_WG * w + 2 * lane + 1] = x1;
           } else {
             ll_store(P.ws, slot_x((d.layer + 1) & 1, 2 * w + lane), pack_h2(x0, x1), tag_of(epoch, d.layer, SID_X));
           }
         }
+        trace_mark(P, d.token, fin_in_token, TR_FINAL);
       }
       break;
     }
-    default: {  // C_LMH chunk
-      if (d.chunk == 0) {
+    default: {  // C_LMH chunk: this wave's 6 rows of chunk d.chunk
+      if (d.chunk < 2) {  // first chunk this wave sees in this token
         cs.lm_best = -INFINITY;
         cs.lm_idx = 0x7fffffff;
       }
       const int nrows = lm_rows(w), r0 = lm_row0(w);
+      float part[LM_ROWS_PER_CHUNK];
 #pragma unroll
-      for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i) {
-        const int lr = lm_local_row(c, d.chunk, i);
-        float sum = dot8(b.v[2 * i], in + 8 * lane) + dot8(b.v[2 * i + 1], in + 512 + 8 * lane);
-        sum = wave_sum(sum);
+      for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i)
+        part[i] = dot8(b.v[2 * i], in + 8 * lane) + dot8(b.v[2 * i + 1], in + 512 + 8 * lane);
+      float pr, qr;
+      reduce6(part, pr, qr);
+      // lane 0: rows 0 (pr), 2 (qr); lane 16: row 1; lane 32: rows 3 (pr), 5 (qr); lane 48: row 4.
+      // Each lane's rows ascend across chunks, so strict > keeps the lowest index.
+      if ((lane & 15) == 0) {
+        const int ip = (lane >> 4) + ((lane >> 4) >= 2 ? 1 : 0);
+        const int lr = lm_local_row(m, d.chunk, ip);
         if (lr < nrows) {
-          const int row = r0 + lr;
-          if (P.logits_out && lane == 0) P.logits_out[(long)d.token * VOCAB + row] = sum;
-          if (sum > cs.lm_best) {  // rows ascend within a wave: strict > keeps the lowest index
-            cs.lm_best = sum;
-            cs.lm_idx = row;
+          if (P.logits_out) P.logits_out[(long)d.token * VOCAB + r0 + lr] = pr;
+          const float v = __builtin_isnan(pr) ? -INFINITY : pr;
+          if (v > cs.lm_best) {
+            cs.lm_best = v;
+            cs.lm_idx = r0 + lr;
           }
         }
       }
-      if (d.chunk == LM_CHUNKS - 1) {
-        if (lane == 0) {
-          red[2 * c] = cs.lm_best;
-          red[2 * c + 1] = __int_as_float(cs.lm_idx);
+      if ((lane & 31) == 0) {
+        const int lr = lm_local_row(m, d.chunk, lane == 0 ? 2 : 5);
+        if (lr < nrows) {
+          if (P.logits_out) P.logits_out[(long)d.token * VOCAB + r0 + lr] = qr;
+          const float v = __builtin_isnan(qr) ? -INFINITY : qr;
+          if (v > cs.lm_best) {
+            cs.lm_best = v;
+            cs.lm_idx = r0 + lr;
+          }
         }
-        if (arrive(S, fin)) {
-          if (lane == 0) {
-            float best = -INFINITY;
-            int bidx = 0x7fffffff;
-            for (int cc = 0; cc < NCW; ++cc) {
-              const float v = red[2 * cc];
-              const int ix = __float_as_int(red[2 * cc + 1]);
-              if (v > best || (v == best && ix < bidx)) {
-                best = v;
-                bidx = ix;
-              }
+      }
+      if (d.chunk >= LM_CHUNKS - 2) {  // this wave's last chunk of the token
+        float bv = cs.lm_best;
+        int bi = cs.lm_idx;
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+          red[2 * c] = bv;
+          red[2 * c + 1] = __int_as_float(bi);
+        }
+        if (arrive(S, fin, NCW)) {
+          float best = -INFINITY;
+          int bidx = 0x7fffffff;
+          for (int cc = 0; cc < NCW; ++cc) {
+            const float v = red[2 * cc];
+            const int ix = __float_as_int(red[2 * cc + 1]);
+            if (v > best || (v == best && ix < bidx)) {
+              best = v;
+              bidx = ix;
             }
+          }
+          mark_done(S, fin);
+          if (lane == 0) {
             const u32 tg = tag_arg(epoch);
             ll_store(P.ws, slot_arg(d.token & 1, 2 * w), __float_as_uint(best), tg);
             ll_store(P.ws, slot_arg(d.token & 1, 2 * w + 1), (u32)bidx, tg);
           }
+          trace_mark(P, d.token, fin_in_token, TR_FINAL);
         }
       }
       break;
@@ -926,31 +1109,26 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
   }
 }
 
+// Compute wave c of group c / 4 (member c % 4) runs the stages j with j % 2 == group.
+// Its single register buffer holds stage j's weights, loaded right after it computed
+// stage j - 2: the only loads in flight when it computes are the ones it needs, so the
+// compiler's wait for them never waits on a later prefetch.
 __device__ void compute_wave(const KParams& P, Shared* S, int c) {
   const int w = blockIdx.x;
   const int lane = __lane_id();
   const int L = P.num_layers;
+  const int grp = c / NGW, m = c % NGW;
   const int total = stages_per_token(P.mode, L) * P.num_steps;
   const u64 deadline = 2 * P.deadline;
-  Buf b0, b1, b2;
+  Buf b;
   CState cs{-INFINITY, 0x7fffffff};
-  if (total > 0) prefetch(P, stage_desc(P.mode, L, 0), b0, w, c, lane);
-  if (total > 1) prefetch(P, stage_desc(P.mode, L, 1), b1, w, c, lane);
-#define QWEN_STEP(CUR, NXT2, OFF)                                                 \
-  {                                                                               \
-    const int j = i + (OFF);                                                      \
-    if (j >= total) break;                                                        \
-    if (j + 2 < total) prefetch(P, stage_desc(P.mode, L, j + 2), NXT2, w, c, lane); \
-    const StageDesc d = stage_desc(P.mode, L, j);                                 \
-    if (!wait_ready(S, (u32)d.fin, deadline)) break;                              \
-    compute(P, S, d, CUR, cs, w, c, lane);                                        \
+  if (grp < total) prefetch(P, stage_desc(P.mode, L, grp), b, w, m, lane);
+  for (int j = grp; j < total; j += 2) {
+    const StageDesc d = stage_desc(P.mode, L, j);
+    if (!wait_ready(S, (u32)d.fin, deadline)) break;
+    compute(P, S, d, b, cs, w, m, c, lane);
+    if (j + 2 < total) prefetch(P, stage_desc(P.mode, L, j + 2), b, w, m, lane);
   }
-  for (int i = 0; i < total; i += 3) {
-    QWEN_STEP(b0, b2, 0)
-    QWEN_STEP(b1, b0, 1)
-    QWEN_STEP(b2, b1, 2)
-  }
-#undef QWEN_STEP
 }
 
 __global__ void __launch_bounds__(BLOCK, 1) qwen_decode_kernel(KParams P) {
@@ -962,6 +1140,8 @@ __global__ void __launch_bounds__(BLOCK, 1) qwen_decode_kernel(KParams P) {
     S.ready = 0;
     S.cnt[0] = 0;
     S.cnt[1] = 0;
+    S.done[0] = 0;
+    S.done[1] = 0;
     S.abort = 0;
   }
   __syncthreads();
@@ -985,6 +1165,8 @@ struct DeviceState {
   u32* status = nullptr;
   u32 epoch = 1;
   u64 deadline = 0;
+  u64* trace = nullptr;
+  int trace_token = -1;
 };
 
 std::mutex g_mu;
@@ -1035,6 +1217,8 @@ int launch(KParams& P, hipStream_t stream) {
   P.ws = st->ws;
   P.status = st->status;
   P.deadline = st->deadline;
+  P.trace = st->trace;
+  P.trace_token = st->trace_token;
   P.epoch0 = st->epoch;
   // epochs are 24-bit in the tag; wrap back to 1 (never 0: a zeroed slot is never "ready")
   u64 next = (u64)st->epoch + (u64)P.num_steps + 1;
@@ -1215,3 +1399,15 @@ extern "C" int qwen_last_error(void) {
 }
 
 extern "C" int qwen_abi_version(void) { return QWEN_ABI_VERSION; }
+
+extern "C" int qwen_set_trace(unsigned long long* buf, int token) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceState* st = nullptr;
+  int rc = device_state(&st);
+  if (rc != QWEN_OK) return rc;
+  st->trace = buf;
+  st->trace_token = buf ? token : -1;
+  return QWEN_OK;
+}
+
+extern "C" int qwen_trace_events(void) { return TRACE_EVENTS; }

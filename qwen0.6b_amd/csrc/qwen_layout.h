@@ -37,6 +37,7 @@ constexpr int MAX_LAYERS = 28;
 
 constexpr int NWG = 256;          // workgroups = CUs
 constexpr int NCW = 8;            // compute waves per workgroup
+constexpr int NGW = 4;            // compute waves per group; stage j runs on group j % 2
 constexpr int WAVE = 64;
 constexpr int BLOCK = (NCW + 1) * WAVE;  // 8 compute waves + 1 exchange wave
 constexpr int NSPLIT = NWG / NKV;  // 32 position splits per kv head
@@ -49,13 +50,13 @@ constexpr int INT_PER_WG = INTER / NWG;     // 12
 constexpr int LM_BASE = VOCAB / NWG;        // 593
 constexpr int LM_EXTRA = VOCAB % NWG;       // 128
 constexpr int LM_MAX_ROWS = LM_BASE + 1;    // 594
-constexpr int LM_ROWS_PER_CHUNK = 3;        // rows per wave per pipeline stage
-constexpr int LM_CHUNKS = (LM_MAX_ROWS + NCW * LM_ROWS_PER_CHUNK - 1) / (NCW * LM_ROWS_PER_CHUNK);  // 25
+constexpr int LM_ROWS_PER_CHUNK = 6;        // rows per wave per pipeline stage
+constexpr int LM_CHUNKS = (LM_MAX_ROWS + NGW * LM_ROWS_PER_CHUNK - 1) / (NGW * LM_ROWS_PER_CHUNK);  // 25
 
 QL_HD int lm_row0(int w) { return LM_BASE * w + (w < LM_EXTRA ? w : LM_EXTRA); }
 QL_HD int lm_rows(int w) { return LM_BASE + (w < LM_EXTRA ? 1 : 0); }
-// local lm_head row handled by compute wave c, chunk k, slot i (may be >= lm_rows)
-QL_HD int lm_local_row(int c, int k, int i) { return c + NCW * (LM_ROWS_PER_CHUNK * k + i); }
+// local lm_head row handled by group member m (0..3), chunk k, slot i (may be >= lm_rows)
+QL_HD int lm_local_row(int m, int k, int i) { return NGW * LM_ROWS_PER_CHUNK * k + LM_ROWS_PER_CHUNK * m + i; }
 
 // QKV row r -> (matrix 0/1/2 = q/k/v, row within it)
 QL_HD int qkv_matrix(int r) { return r < QSZ ? 0 : (r < QSZ + KVSZ ? 1 : 2); }
@@ -71,8 +72,8 @@ QL_HD int att_t1(int ctx, int s) {
   int e = att_t0(ctx, s) + att_span(ctx);
   return e < ctx ? e : ctx;
 }
-// position within the split handled by compute wave c, lane group j (0..3), half b (0..1)
-QL_HD int att_local_pos(int c, int j, int b) { return 8 * c + j + 4 * b; }
+// position within the split handled by group member m (0..3), lane group j (0..3), slot b (0..3)
+QL_HD int att_local_pos(int m, int j, int b) { return 16 * m + j + 4 * b; }
 
 // combine role
 QL_HD int cmb_head(int w) { return w / 16; }

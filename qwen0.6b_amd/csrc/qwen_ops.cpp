@@ -188,6 +188,16 @@ torch::Tensor mlp_block(torch::Tensor x, torch::Tensor post_norm, torch::Tensor 
 
 int last_error() { return qwen_last_error(); }
 
+void set_trace(c10::optional<torch::Tensor> buf, int token) {
+  if (!buf.has_value()) {
+    check_rc(qwen_set_trace(nullptr, -1), "set_trace");
+    return;
+  }
+  TORCH_CHECK(buf->is_cuda() && buf->scalar_type() == torch::kLong && buf->is_contiguous(),
+              "trace buffer must be a contiguous int64 GPU tensor");
+  check_rc(qwen_set_trace(reinterpret_cast<unsigned long long*>(buf->data_ptr<int64_t>()), token), "set_trace");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(qwen_megakernel_C, m) {
@@ -206,4 +216,7 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
         pybind11::arg("weight"), pybind11::arg("logits_out") = pybind11::none());
   m.def("mlp_block", &mlp_block, "isolated RMSNorm + SwiGLU MLP + residual");
   m.def("last_error", &last_error, "synchronize and return the device-side error state (0 = ok)");
+  m.def("set_trace", &set_trace, "record per-stage device timestamps of one token into an int64 GPU tensor "
+        "[256, fins, events] (None to stop)", pybind11::arg("buf"), pybind11::arg("token") = 0);
+  m.def("trace_events", &qwen_trace_events, "events recorded per stage by set_trace");
 }
