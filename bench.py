@@ -80,6 +80,9 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after timing, run 3 device-to-device copies of 1 GiB (torch copy_) so a counter "
+                         "run can scale FETCH_SIZE / WRITE_SIZE against a kernel of known traffic")
     ap.add_argument("--trace", default=None,
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
                          "into this .npy file ([256 workgroups, 141 stages, 4 events], 100 MHz ticks)")
@@ -144,6 +147,15 @@ def main():
         ext.set_trace(None, 0)
         np.save(args.trace, buf.view(256, fins, ext.trace_events()).cpu().numpy())
         log(f"trace written to {args.trace}")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.float16, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("copy calibration: 3 x 1 GiB copies done")
 
     value = NEW * args.steps / elapsed
     avg_kernel_s = sum(kernel_ms) / len(kernel_ms) / 1e3

@@ -21,6 +21,12 @@ INC = os.path.join(REPO, "include")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# SimplifyCFG's common-code sinking merges the per-stage-type stores into the
+# compute waves' weight prefetch buffer into one store through a phi of
+# addresses, which pins that buffer in scratch memory: every prefetch then waits
+# for its loads (vmcnt(0)) to spill them and every stage reloads them from
+# memory. With sinking off the buffer stays in VGPRs.
+NO_SINK = ["-mllvm", "-simplifycfg-sink-common=false"]
 
 
 def _run(cmd):
@@ -31,7 +37,7 @@ def _run(cmd):
 def build_kernels():
     out = os.path.join(HERE, "libqwen_megakernel.so")
     _run([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", f"-I{INC}", f"-I{CSRC}",
-          *NO_PACKED_FP32, os.path.join(CSRC, "megakernel.hip"), "-o", out])
+          *NO_PACKED_FP32, *NO_SINK, os.path.join(CSRC, "megakernel.hip"), "-o", out])
     return out
 
 

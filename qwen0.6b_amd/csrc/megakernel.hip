@@ -466,17 +466,17 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           const h4 sv = *(const h4*)(P.sin_t + (long)pos * HD + d0);
           const h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d0);
           const h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d0);
-          v4u v[2];
-          // pair k = 0: q slots 128g + 2 lane; k = 1: k slots (lane < 32) or v slots (lane >= 32)
+          v4u vq[1], vkv[1];
+          // q slots 128g + 2 lane; k slots (lane < 32) or v slots (lane >= 32)
           poll_pairs<1>(pl, tag_of(epoch, l, SID_QKV), attq_voff(lane), true,
-                        [&](int) -> int { return (int)attq_soff(par, g); }, *(v4u(*)[1])&v[0]);
+                        [&](int) -> int { return (int)attq_soff(par, g); }, vq);
           poll_pairs<1>(pl, tag_of(epoch, l, SID_QKV), attkv_voff(lane), true,
-                        [&](int) -> int { return (int)attkv_soff(par, g); }, *(v4u(*)[1])&v[1]);
+                        [&](int) -> int { return (int)attkv_soff(par, g); }, vkv);
           if (!pl.ok) break;
-          // k = 0: q values 4 lane .. (q head 2g for lane < 32, 2g+1 above)
-          // k = 1: lane < 32: k dims 4 lane.., lane >= 32: v dims 4(lane-32)..
-          float q[4] = {lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z)};
-          float kv[4] = {lo_h(v[1].x), hi_h(v[1].x), lo_h(v[1].z), hi_h(v[1].z)};
+          // vq: q values 4 lane .. (q head 2g for lane < 32, 2g+1 above)
+          // vkv: lane < 32: k dims 4 lane.., lane >= 32: v dims 4(lane-32)..
+          float q[4] = {lo_h(vq[0].x), hi_h(vq[0].x), lo_h(vq[0].z), hi_h(vq[0].z)};
+          float kv[4] = {lo_h(vkv[0].x), hi_h(vkv[0].x), lo_h(vkv[0].z), hi_h(vkv[0].z)};
           // q head norms (each 32-lane half is one head)
           float ssq = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
           ssq = half_sum(ssq);
@@ -551,9 +551,11 @@ __device__ void exchange_wave(const KParams& P, Shared* S) {
           const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
           // drain the KV-cache stores before any workgroup can depend on this step
           __builtin_amdgcn_s_waitcnt(0);
+          // lane k < 4 stores dims 2k, 2k+1 (static selects: no lane-indexed array)
+          const float oa = lane == 0 ? o[0] : (lane == 1 ? o[2] : (lane == 2 ? o[4] : o[6]));
+          const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
           if (lane < 4)
-            ll_store(P.ws, slot_att(par, 4 * w + lane), pack_h2(o[2 * lane] * inv, o[2 * lane + 1] * inv),
-                     tag_of(epoch, l, SID_ATT));
+            ll_store(P.ws, slot_att(par, 4 * w + lane), pack_h2(oa * inv, ob * inv), tag_of(epoch, l, SID_ATT));
           xtrace(P, t, fin - (u32)(t * FT), TR_COMBINE);
         }
 
