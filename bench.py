@@ -43,6 +43,22 @@ def algorithmic_bytes(start, n):
     return total
 
 
+TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "qwen_decode_kernel.ctx2048.hbm_counters.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of this workload from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled against a copy kernel of known size), or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -189,7 +205,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "qwen_decode_kernel",
             "bytes_per_launch": per_launch,
             "kernel_ms": round(avg_kernel_s * 1e3, 3),

@@ -50,8 +50,16 @@ constexpr float RMS_EPS = 1e-6f;
 constexpr u32 ST_TIMEOUT = 1u;
 constexpr u32 ST_BAD_TOKEN = 2u;
 // optional device timestamps (wall clock) per workgroup and finalised stage of one token
-constexpr int TRACE_EVENTS = 4;
-enum TraceEvent : int { TR_POLL = 0, TR_PUBLISH = 1, TR_FINAL = 2, TR_COMBINE = 3 };
+constexpr int TRACE_EVENTS = 8;
+enum TraceEvent : int {
+  TR_POLL = 0,     // exchange wave starts waiting for the stage input
+  TR_PUBLISH = 1,  // stage input handed to the compute waves
+  TR_FINAL = 2,    // stage results stored
+  TR_COMBINE = 3,  // attention merge stored / argmax known
+  TR_CSTART = 4,   // compute wave 0 of the stage's group saw the input
+  TR_CDONE = 5,    // compute wave 0 of the stage's group finished the stage
+  TR_FSTART = 6,   // the finalising wave starts finalising
+};
 
 struct KParams {
   const _Float16* embed;
@@ -820,6 +828,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
       const float rs = reduce4(part[0], part[1], part[2], part[3]);
       if ((lane & 15) == 0) red[4 * m + ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : (lane >> 4)))] = rs;
       if (arrive(S, fin, NGW)) {
+        trace_mark(P, d.token, fin_in_token, TR_FSTART);
         float v0 = 0.f, v1 = 0.f;
         if (lane < QKV_PER_WG / 2) {
           v0 = red[2 * lane];
@@ -923,6 +932,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
         rec[131] = lh[1];
       }
       if (arrive(S, fin, NGW)) {
+        trace_mark(P, d.token, fin_in_token, TR_FSTART);
         // merge the 4 wave partials into the workgroup partial (m, l, acc) per head
         float Mx[2], wt[2][NGW];
 #pragma unroll
@@ -975,6 +985,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
       sum = wave_sum(sum);
       if (lane == 0) red[m] = sum;
       if (arrive(S, fin, NGW)) {
+        trace_mark(P, d.token, fin_in_token, TR_FSTART);
         float a0 = 0.f, a1 = 0.f;
         if (lane < 2) {
           const int r0 = 2 * lane;
@@ -998,6 +1009,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
       if ((lane & 15) == 0) red[6 * m + (lane >> 4) + ((lane >> 4) >= 2 ? 1 : 0)] = pr;
       if ((lane & 31) == 0) red[6 * m + (lane == 0 ? 2 : 5)] = qr;
       if (arrive(S, fin, NGW)) {
+        trace_mark(P, d.token, fin_in_token, TR_FSTART);
         float o[2] = {0.f, 0.f};
         if (lane < INT_PER_WG / 2) {
 #pragma unroll
@@ -1020,6 +1032,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
       sum = wave_sum(sum);
       if (lane == 0) red[m] = sum;
       if (arrive(S, fin, NGW)) {
+        trace_mark(P, d.token, fin_in_token, TR_FSTART);
         float x0 = 0.f, x1 = 0.f;
         if (lane < 2) {
           const int r0 = 2 * lane;
@@ -1087,6 +1100,7 @@ __device__ __forceinline__ void compute(const KParams& P, Shared* S, const Stage
           red[2 * c + 1] = __int_as_float(bi);
         }
         if (arrive(S, fin, NCW)) {
+          trace_mark(P, d.token, fin_in_token, TR_FSTART);
           float best = -INFINITY;
           int bidx = 0x7fffffff;
           for (int cc = 0; cc < NCW; ++cc) {
@@ -1128,7 +1142,10 @@ __device__ void compute_wave(const KParams& P, Shared* S, int c) {
   for (int j = grp; j < total; j += 2) {
     const StageDesc d = stage_desc(P.mode, L, j);
     if (!wait_ready(S, (u32)d.fin, deadline)) break;
+    const u32 fin_in_token = (u32)d.fin - (u32)(d.token * fins_per_token(P.mode, L));
+    if (m == 0) trace_mark(P, d.token, fin_in_token, TR_CSTART);
     compute(P, S, d, b, cs, w, m, c, lane);
+    if (m == 0) trace_mark(P, d.token, fin_in_token, TR_CDONE);
     if (j + 2 < total) prefetch(P, stage_desc(P.mode, L, j + 2), b, w, m, lane);
   }
 }
