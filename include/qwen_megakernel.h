@@ -139,12 +139,14 @@ int qwen_last_error(void);
 int qwen_abi_version(void);
 
 /* Profiling aid: while buf is non-null, every launch on the current device
- * records wall-clock timestamps (s_memrealtime ticks) for token index `token`
- * of the launch into buf[workgroup][finalised stage][qwen_trace_events()]
- * (device u64, 256 x (5*num_layers+1) x events). Events: 0 = exchange wave
- * starts polling the stage input, 1 = input handed to the compute waves,
- * 2 = the stage's results stored, 3 = attention merge stored / argmax known.
- * Pass buf = NULL to stop. */
+ * records wall-clock timestamps (s_memrealtime ticks, 100 MHz) for token index
+ * `token` of the launch into buf[workgroup][stage][qwen_trace_events()]
+ * (device u64, 256 x (8*num_layers+1) x events; stage 8*l + s is stage s of
+ * layer l in the order QKV, attention, combine, o_proj, o_proj sum, gate/up,
+ * down, down sum; stage 8*num_layers is the lm_head input and argmax).
+ * Events, all from compute wave 0 of the workgroup: 0 = starts waiting for the
+ * stage input, 1 = has its quarter of the input, 2 = passed the compute-wave
+ * barrier, 3 = stored its results. Pass buf = NULL to stop. */
 int qwen_set_trace(unsigned long long* buf, int token);
 int qwen_trace_events(void);
 

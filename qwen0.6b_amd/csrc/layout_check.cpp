@@ -1,7 +1,9 @@
 // Exhaustive CPU check of every index the decode kernel forms (qwen_layout.h):
 // work partitions cover their ranges exactly once, every exchange-slot read and
-// write stays inside its own buffer, poll offsets address the intended slots,
-// and the stage sequence is consistent. Exit status 0 = all checks passed.
+// write stays inside its own buffer, the poll addresses (per-lane offset +
+// wave-uniform base, exactly as the kernel forms them) hit the intended slots,
+// ring lines stay inside their matrices, and the attention split schedule
+// covers every context. Exit status 0 = all checks passed.
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -11,245 +13,296 @@
 using namespace ql;
 
 static int g_fail = 0;
-#define CHECK(cond, ...)                          \
-  do {                                            \
-    if (!(cond)) {                                \
-      if (g_fail < 20) {                          \
+#define CHECK(cond, ...)                                     \
+  do {                                                       \
+    if (!(cond)) {                                           \
+      if (g_fail < 20) {                                     \
         fprintf(stderr, "FAIL %s:%d: ", __FILE__, __LINE__); \
-        fprintf(stderr, __VA_ARGS__);             \
-        fprintf(stderr, "\n");                    \
-      }                                           \
-      ++g_fail;                                   \
-    }                                             \
+        fprintf(stderr, __VA_ARGS__);                        \
+        fprintf(stderr, "\n");                               \
+      }                                                      \
+      ++g_fail;                                              \
+    }                                                        \
   } while (0)
 
 static bool in_buf(long slot, long off, long n) { return slot >= off && slot < off + n; }
 
 int main() {
-  // buffers: disjoint, in order, inside the workspace, pair-aligned
-  const long offs[] = {OFF_X, OFF_QKV, OFF_PART, OFF_ATT, OFF_ACT, OFF_INT, OFF_ARG, TOTAL_SLOTS};
-  const long sizes[] = {2L * X_SLOTS, 2L * QKV_SLOTS, 2L * PART_SLOTS, 2L * ATT_SLOTS,
-                        2L * ACT_SLOTS, 2L * INT_SLOTS, 2L * ARG_SLOTS};
-  for (int b = 0; b < 7; ++b) {
+  // ---- exchange layout: buffers contiguous, pair-aligned, inside the workspace ----
+  const long offs[] = {B_X, B_QKV, B_PART, B_ATTO, B_OP, B_ACT, B_INT, B_DP, XCD_SLOTS};
+  const long sizes[] = {X_SLOTS, QKV_SLOTS, PART_SLOTS, ATTO_SLOTS, OP_SLOTS, ACT_SLOTS, INT_SLOTS, DP_SLOTS};
+  for (int b = 0; b < 8; ++b) {
     CHECK(offs[b] + sizes[b] == offs[b + 1], "buffer %d not contiguous", b);
-    CHECK(offs[b] % 2 == 0, "buffer %d base not pair aligned", b);
+    CHECK(offs[b] % 2 == 0 && sizes[b] % 2 == 0, "buffer %d not pair aligned", b);
   }
-  CHECK(TOTAL_SLOTS * 8 + 256 == WORKSPACE_BYTES, "workspace size");
-  CHECK(WORKSPACE_BYTES < (1L << 31), "workspace offsets must fit the 32-bit buffer offset");
-  CHECK(BLOCK == 576 && NWG * QKV_PER_WG == QKV_ROWS && NWG * HID_PER_WG == HIDDEN && NWG * INT_PER_WG == INTER,
-        "partition constants");
+  CHECK(XCD_SLOTS % 2 == 0 && OFF_ARG % 2 == 0, "xcd / arg alignment");
+  CHECK(xbuf(1, NXCD - 1, XCD_SLOTS) == OFF_ARG, "xcd buffers end at the ARG buffer");
+  CHECK(OFF_ARG + 2L * ARG_SLOTS == TOTAL_SLOTS, "ARG end");
+  CHECK(TOTAL_SLOTS * 8 + 256 == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
+  CHECK(BLOCK == 512 && NLOC == 32 && NXCD * NLOC == NWG, "grid constants");
+  for (int w = 0; w < NWG; ++w) CHECK(8 * loc_of(w) + xcd_of(w) == w, "w = 8 i + x");
 
-  // QKV rows: each of the 4096 rows exactly once; matrix/row mapping in range
+  // ---- QKV rows: over all (x, i, c, r) each row of Wq, Wk, Wv exactly once ----
   {
-    std::vector<int> seen(QKV_ROWS, 0);
-    for (int w = 0; w < NWG; ++w)
-      for (int m = 0; m < NGW; ++m)
-        for (int r = 0; r < 4; ++r) {
-          int row = QKV_PER_WG * w + 4 * m + r;
-          CHECK(row < QKV_ROWS, "qkv row");
-          seen[row]++;
-          int mat = qkv_matrix(row), ri = qkv_row_in(row);
-          int lim = mat == 0 ? QSZ : KVSZ;
-          CHECK(ri >= 0 && ri < lim, "qkv row_in %d", row);
-          CHECK((mat == 0 ? ri : (mat == 1 ? QSZ + ri : QSZ + KVSZ + ri)) == row, "qkv map %d", row);
-        }
-    for (int r = 0; r < QKV_ROWS; ++r) CHECK(seen[r] == 1, "qkv row %d seen %d", r, seen[r]);
-    // finalize slots: slot 8w + lane holds rows 16w + 2 lane, +1
-    for (int w = 0; w < NWG; ++w)
-      for (int lane = 0; lane < QKV_PER_WG / 2; ++lane)
-        for (int par = 0; par < 2; ++par) {
-          long s = slot_qkv(par, (QKV_PER_WG / 2) * w + lane);
-          CHECK(in_buf(s, OFF_QKV + par * QKV_SLOTS, QKV_SLOTS), "qkv slot");
-        }
+    std::vector<int> q(QSZ, 0), k(KVSZ, 0), v(KVSZ, 0);
+    for (int x = 0; x < NXCD; ++x)
+      for (int i = 0; i < NLOC; ++i)
+        for (int c = 0; c < NCW; ++c)
+          for (int r = 0; r < 4; ++r) {
+            const int gr = QKV_PER_WG * i + 4 * c + r;
+            CHECK(gr < GRP_ROWS, "group row");
+            const int mat = grp_matrix(gr), row = grp_row_in(x, gr);
+            if (mat == 0) {
+              CHECK(row >= 0 && row < QSZ && row / HD == 2 * x + gr / HD, "q row %d", row);
+              if (row >= 0 && row < QSZ) q[row]++;
+            } else {
+              CHECK(row >= 0 && row < KVSZ && row / HD == x, "k/v row %d", row);
+              if (row >= 0 && row < KVSZ) (mat == 1 ? k : v)[row]++;
+            }
+            // the store slot holds group rows 2s, 2s+1 of this workgroup's 16
+            const int slot = (QKV_PER_WG / 2) * i + 2 * c + r / 2;
+            CHECK(2 * slot + (r & 1) == gr && slot < QKV_SLOTS, "qkv slot");
+          }
+    for (int r = 0; r < QSZ; ++r) CHECK(q[r] == 1, "q row %d seen %d", r, q[r]);
+    for (int r = 0; r < KVSZ; ++r) CHECK(k[r] == 1 && v[r] == 1, "k/v row %d", r);
+    // ring lines of the QKV stage: line m = row m / 2, half m % 2
+    for (int m = 0; m < LINES_QKV; ++m) CHECK((m >> 1) < QKV_PER_WG, "qkv line");
   }
 
-  // attention input poll: load 0 / load 1 address exactly att_in_slot(g, 2(lane + 64k))
-  for (int par = 0; par < 2; ++par)
-    for (int g = 0; g < NKV; ++g) {
-      std::vector<int> seen(256, 0);
-      for (int lane = 0; lane < WAVE; ++lane) {
-        long b0 = attq_voff(lane) + attq_soff(par, g);
-        long b1 = attkv_voff(lane) + attkv_soff(par, g);
-        CHECK(b0 % 16 == 0 && b1 % 16 == 0, "att poll alignment");
-        CHECK(b0 == slot_qkv(par, att_in_slot(g, 2 * lane)) * 8, "att q poll g%d lane%d", g, lane);
-        CHECK(b1 == slot_qkv(par, att_in_slot(g, 2 * (lane + 64))) * 8, "att kv poll g%d lane%d", g, lane);
-        for (int k = 0; k < 2; ++k) {
-          int c = 2 * (lane + 64 * k);
-          seen[c]++;
-          seen[c + 1]++;
-          // the pair never straddles a q|k|v segment
-          CHECK(att_in_slot(g, c + 1) == att_in_slot(g, c) + 1, "att pair contiguity");
+  // ---- attention input poll: quarter c, lane < 32 -> values 4 (32 c + lane) .. +4 ----
+  {
+    std::vector<int> seen(GRP_ROWS, 0);
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < 32; ++lane) {
+        const long slot = 64 * c + (16 * lane) / 8;  // soff / 8 relative to the buffer + voff / 8
+        CHECK(slot % 2 == 0 && slot + 1 < QKV_SLOTS, "att poll range");
+        for (int e = 0; e < 4; ++e) {
+          const int val = 2 * (int)slot + e;
+          CHECK(val == 128 * c + 4 * lane + e, "att vin index");
+          seen[val]++;
         }
       }
-      for (int c = 0; c < 256; ++c) CHECK(seen[c] == 1, "att input %d", c);
-      // q slots hold q heads 2g, 2g+1; k slots k head g; v slots v head g
-      for (int c = 0; c < 256; ++c) {
-        int slot = att_in_slot(g, c), v0 = 2 * slot;  // first value index in the 4096-vector
-        if (c < 128) CHECK(v0 >= 256 * g && v0 < 256 * g + 256, "q segment");
-        else if (c < 192) CHECK(v0 >= QSZ + 128 * g && v0 < QSZ + 128 * g + 128, "k segment");
-        else CHECK(v0 >= QSZ + KVSZ + 128 * g && v0 < QSZ + KVSZ + 128 * g + 128, "v segment");
-      }
-    }
+    for (int e = 0; e < GRP_ROWS; ++e) CHECK(seen[e] == 1, "att input %d", e);
+  }
 
-  // attention positions: every position of every context exactly once, <= 64 per split
-  for (int ctx = 1; ctx <= NSPLIT * MAX_SPLIT_POS; ++ctx) {
-    CHECK(att_span(ctx) <= MAX_SPLIT_POS, "span ctx %d", ctx);
+  // ---- attention split schedule: every position of every context exactly once ----
+  for (int ctx = 1; ctx <= MAX_SEQ_LIMIT; ++ctx) {
+    const int pos = ctx - 1;
     std::vector<int> seen(ctx, 0);
+    int holders = 0;
     for (int s = 0; s < NSPLIT; ++s) {
-      int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s);
-      for (int m = 0; m < NGW; ++m)
-        for (int j = 0; j < 4; ++j)
-          for (int b = 0; b < 4; ++b) {
-            int lp = att_local_pos(m, j, b);
-            CHECK(lp >= 0 && lp < MAX_SPLIT_POS, "local pos");
-            int p = t0 + lp;
-            if (p < t1) {
+      const int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s), nk = att_nk(ctx, s);
+      CHECK(t0 % 4 == 0 && t1 >= t0 && t1 <= (ctx > t0 ? ctx : t0), "split range ctx %d s %d", ctx, s);
+      CHECK(nk <= 16 && 2 * nk <= RING_LINES, "split lines ctx %d", ctx);
+      CHECK(nk == 0 || (t0 + 4 * nk >= t1 && t0 + 4 * (nk - 1) < t1), "nk covers the split");
+      holders += (t0 <= pos && pos < t1);
+      // positions the compute waves treat as valid: m = 4c + bb < nk, p = t0 + 4m + j < t1
+      for (int c = 0; c < NCW; ++c)
+        for (int bb = 0; bb < 4; ++bb)
+          for (int j = 0; j < 4; ++j) {
+            const int m = 4 * c + bb, p = t0 + 4 * m + j;
+            if (m < nk && p < t1) {
               CHECK(p >= 0 && p < ctx, "pos range");
               seen[p]++;
             }
           }
+      // loader: cached positions p < min(t1, pos), inside the cache rows
+      for (int m = 0; m < nk; ++m)
+        for (int lane = 0; lane < WAVE; ++lane) {
+          const int p = t0 + 4 * m + (lane >> 4);
+          const int lim = t1 < pos ? t1 : pos;
+          if (p < lim) CHECK(p >= 0 && p < pos && p < MAX_SEQ_LIMIT, "cached position");
+        }
     }
     for (int p = 0; p < ctx; ++p) CHECK(seen[p] == 1, "ctx %d pos %d seen %d", ctx, p, seen[p]);
-    // exactly one split holds the newest position
-    int holders = 0;
-    for (int s = 0; s < NSPLIT; ++s) holders += (att_t0(ctx, s) <= ctx - 1 && ctx - 1 < att_t1(ctx, s));
     CHECK(holders == 1, "pos holder ctx %d", ctx);
   }
-  // each (kv head, split) pair is one workgroup
+
+  // ---- attention partial stores and the combine poll ----
   {
-    std::vector<int> seen(NWG, 0);
-    for (int w = 0; w < NWG; ++w) seen[att_kv(w) * NSPLIT + att_split(w)]++;
-    for (int i = 0; i < NWG; ++i) CHECK(seen[i] == 1, "att role %d", i);
+    for (int i = 0; i < NLOC; ++i)
+      for (int c = 0; c < NCW; ++c)
+        for (int it = 0; it < 2; ++it)
+          for (int lane = 0; lane < WAVE; ++lane) {
+            if (it == 1 && lane != 0) continue;
+            const int e = 65 * c + (it == 0 ? lane : 64);
+            const int h = e >= PART_PER_HEAD ? 1 : 0, k = e - PART_PER_HEAD * h;
+            CHECK(e < 2 * PART_PER_HEAD && k >= 0 && k < PART_PER_HEAD, "merge entry");
+            CHECK(part_index(i, h, k) < PART_SLOTS, "part slot");
+          }
+    std::vector<int> seen(OCOLS, 0);
+    for (int i = 0; i < NLOC; ++i) {
+      const int hh = i / 16, d0 = 8 * (i % 16);
+      for (int e = 0; e < 8; ++e) seen[hh * HD + d0 + e]++;
+      CHECK(8 * i == hh * HD + d0, "ATTO value order");
+      for (int s = 0; s < NSPLIT; ++s)
+        for (int k = 0; k < 5; ++k) {
+          const long slot = part_index(s, hh, k == 0 ? 0 : 2 + d0 + 2 * (k - 1));
+          CHECK(slot % 2 == 0 && slot + 1 < PART_SLOTS, "combine poll");
+        }
+      for (int lane = 0; lane < 4; ++lane) CHECK(4 * i + lane < ATTO_SLOTS, "atto slot");
+    }
+    for (int e = 0; e < OCOLS; ++e) CHECK(seen[e] == 1, "combine value %d", e);
   }
-  // partial slots written by the attention finalizer stay in their buffer
+
+  // ---- o_proj: ATTO quarter poll, ring lines, partial rows ----
+  {
+    std::vector<int> seen(OCOLS, 0);
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < 16; ++lane) {
+        const int slot = 32 * c + 2 * lane;
+        CHECK(slot + 1 < ATTO_SLOTS, "atto poll");
+        for (int e = 0; e < 4; ++e) seen[64 * c + 4 * lane + e]++;
+      }
+    for (int e = 0; e < OCOLS; ++e) CHECK(seen[e] == 1, "o input %d", e);
+    std::vector<int> rows(HIDDEN * NXCD, 0);
+    for (int x = 0; x < NXCD; ++x)
+      for (int i = 0; i < NLOC; ++i)
+        for (int m = 0; m < LINES_O; ++m)
+          for (int lane = 0; lane < WAVE; ++lane) {
+            const int row = HROWS * i + 2 * m + (lane >> 5), col = OCOLS * x + 8 * (lane & 31);
+            CHECK(row < HIDDEN && col + 8 <= QSZ && col >= OCOLS * x && col + 8 <= OCOLS * (x + 1), "o line");
+            if ((lane & 31) == 0) rows[x * HIDDEN + row]++;
+          }
+    for (int r = 0; r < HIDDEN * NXCD; ++r) CHECK(rows[r] == 1, "o row %d", r);
+    // compute wave c: lines 4c + m; stored rows 8c + {0,2,1,3} (+4)
+    for (int c = 0; c < NCW; ++c) {
+      std::vector<int> rs(8, 0);
+      for (int l16 = 0; l16 < 4; ++l16) {
+        const int rr = (l16 == 1 ? 2 : (l16 == 2 ? 1 : l16));
+        rs[rr]++;
+        rs[rr + 4]++;
+        // the line holding that row: (rr / 2) within the first pair of lines
+        const int line_y0 = 4 * c + (l16 & 1), half = l16 >> 1;
+        CHECK(2 * line_y0 + half == 8 * c + rr, "o row from y0");
+        const int line_y1 = 4 * c + 2 + (l16 & 1);
+        CHECK(2 * line_y1 + half == 8 * c + rr + 4, "o row from y1");
+      }
+      for (int r = 0; r < 8; ++r) CHECK(rs[r] == 1, "o store rows");
+    }
+  }
+
+  // ---- residual sums: peer poll addresses ----
   for (int par = 0; par < 2; ++par)
-    for (int w = 0; w < NWG; ++w)
-      for (int e = 0; e < 2 * PART_PER_HEAD; ++e) {
-        int h = e >= PART_PER_HEAD, k = e - PART_PER_HEAD * h;
-        long s = slot_part(par, att_kv(w), att_split(w), h, k);
-        CHECK(in_buf(s, OFF_PART + par * PART_SLOTS, PART_SLOTS), "part slot");
-      }
-
-  // combine: 2048 attention outputs exactly once; poll offsets hit (m,l) and acc pairs
-  {
-    std::vector<int> seen(QSZ, 0);
-    for (int w = 0; w < NWG; ++w) {
-      int h = cmb_head(w), d0 = cmb_d0(w);
-      CHECK(h < NQ && d0 + 8 <= HD, "combine role");
-      for (int e = 0; e < 8; ++e) seen[h * HD + d0 + e]++;
-      CHECK(8 * w == h * HD + d0, "combine output slots");
-      for (int par = 0; par < 2; ++par)
-        for (int lane = 0; lane < NSPLIT; ++lane)
-          for (int k = 0; k < 5; ++k) {
-            long b = cmb_voff(lane) + cmb_soff(par, h, d0, k);
-            long expect = slot_part(par, h / 2, lane, h % 2, k == 0 ? 0 : 2 + d0 + 2 * (k - 1)) * 8;
-            CHECK(b == expect && b % 16 == 0, "combine poll w%d lane%d k%d", w, lane, k);
-            CHECK(in_buf(b / 8, OFF_PART + par * PART_SLOTS, PART_SLOTS) &&
-                      in_buf(b / 8 + 1, OFF_PART + par * PART_SLOTS, PART_SLOTS),
-                  "combine poll range");
-          }
-      for (int lane = 0; lane < 4; ++lane)
-        CHECK(in_buf(slot_att(0, 4 * w + lane), OFF_ATT, ATT_SLOTS), "att slot");
-    }
-    for (int i = 0; i < QSZ; ++i) CHECK(seen[i] == 1, "combine out %d", i);
-  }
-
-  // o_proj / down rows (4 per WG, one per group member), gate/up (12 + 12 per WG, 6 per member)
-  {
-    std::vector<int> oseen(HIDDEN, 0), gseen(INTER, 0), useen(INTER, 0);
-    for (int w = 0; w < NWG; ++w) {
-      for (int m = 0; m < NGW; ++m) oseen[HID_PER_WG * w + m]++;
-      for (int m = 0; m < NGW; ++m)
-        for (int k = 0; k < 6; ++k) {
-          int lr = 6 * m + k;
-          int row = INT_PER_WG * w + (lr % INT_PER_WG);
-          (lr < INT_PER_WG ? gseen : useen)[row]++;
-        }
-      for (int lane = 0; lane < 2; ++lane) {
-        CHECK(in_buf(slot_act(1, 2 * w + lane), OFF_ACT + ACT_SLOTS, ACT_SLOTS), "act slot");
-        CHECK(in_buf(slot_x(1, 2 * w + lane), OFF_X + X_SLOTS, X_SLOTS), "x slot");
-      }
-      for (int lane = 0; lane < INT_PER_WG / 2; ++lane)
-        CHECK(in_buf(slot_int(1, (INT_PER_WG / 2) * w + lane), OFF_INT + INT_SLOTS, INT_SLOTS), "int slot");
-      for (int lane = 0; lane < 2; ++lane) CHECK(in_buf(slot_arg(1, 2 * w + lane), OFF_ARG + ARG_SLOTS, ARG_SLOTS), "arg");
-    }
-    for (int i = 0; i < HIDDEN; ++i) CHECK(oseen[i] == 1, "o/down row %d", i);
-    for (int i = 0; i < INTER; ++i) CHECK(gseen[i] == 1 && useen[i] == 1, "gate/up row %d", i);
-    // activation offsets read per lane: 8 lane + 512k + 8 <= 2048 (o_proj, k < 4), <= 3072 (down, k < 6)
-    for (int lane = 0; lane < WAVE; ++lane) {
-      for (int k = 0; k < 4; ++k) CHECK(512 * k + 8 * lane + 8 <= QSZ, "o_proj act index");
-      for (int k = 0; k < 6; ++k) CHECK(512 * k + 8 * lane + 8 <= INTER, "down act index");
-    }
-  }
-
-  // linear polls: pair k of lane covers slots 2(lane+64k), +1 inside the buffer
-  {
-    struct V { long base; int n; const char* name; } vecs[] = {
-        {slot_x(1, 0), X_SLOTS, "x"}, {slot_att(1, 0), ATT_SLOTS, "att"}, {slot_act(1, 0), ACT_SLOTS, "act"},
-        {slot_int(1, 0), INT_SLOTS, "int"}, {slot_arg(1, 0), ARG_SLOTS, "arg"}};
-    for (auto& v : vecs) {
-      std::vector<int> seen(v.n, 0);
-      const int K = v.n / 128;
-      for (int lane = 0; lane < WAVE; ++lane)
-        for (int k = 0; k < K; ++k) {
-          long b = lin_voff(lane) + lin_soff(v.base, k);
-          long s = b / 8 - v.base;
-          CHECK(b % 16 == 0 && s == 2 * (lane + 64 * k), "%s poll address", v.name);
-          CHECK(s >= 0 && s + 1 < v.n, "%s poll range", v.name);
-          if (s >= 0 && s + 1 < v.n) {
-            seen[s]++;
-            seen[s + 1]++;
+    for (int i = 0; i < NLOC; ++i)
+      for (const long B : {B_OP, B_DP}) {
+        std::vector<int> seen(NXCD * HROWS, 0);
+        for (int c = 0; c < NCW; ++c) {
+          const long src0 = xbuf(par, 2 * c, B) + HROWS * i;
+          for (int lane = 0; lane < 32; ++lane) {
+            const long slot = src0 + ((long)((lane >> 4) & 1) * XCD_SLOTS + 2 * (lane & 15));
+            const int g = 2 * c + ((lane >> 4) & 1), r = 2 * (lane & 15);
+            CHECK(slot == xbuf(par, g, B) + HROWS * i + r && slot % 2 == 0, "peer poll address");
+            CHECK(in_buf(slot, xbuf(par, g, B), HIDDEN) && in_buf(slot + 1, xbuf(par, g, B), HIDDEN), "peer range");
+            seen[g * HROWS + r]++;
+            seen[g * HROWS + r + 1]++;
           }
         }
-      for (int i = 0; i < v.n; ++i) CHECK(seen[i] == 1, "%s slot %d read %d", v.name, i, seen[i]);
-    }
+        for (int e = 0; e < NXCD * HROWS; ++e) CHECK(seen[e] == 1, "peer row %d", e);
+      }
+  // residual row stores: ACT / X slots 16 i + 4 c + lane hold rows 32 i + 8 c + 2 lane, +1
+  {
+    std::vector<int> seen(HIDDEN, 0);
+    for (int i = 0; i < NLOC; ++i)
+      for (int c = 0; c < NCW; ++c)
+        for (int lane = 0; lane < 4; ++lane) {
+          const int slot = 16 * i + 4 * c + lane;
+          CHECK(slot < X_SLOTS && 2 * slot == HROWS * i + 8 * c + 2 * lane, "x slot rows");
+          seen[2 * slot]++;
+          seen[2 * slot + 1]++;
+        }
+    for (int r = 0; r < HIDDEN; ++r) CHECK(seen[r] == 1, "x row %d", r);
+    // quarter polls of a 1024-value vector: slots 128 c + 2 lane
+    std::vector<int> got(HIDDEN, 0);
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < WAVE; ++lane) {
+        const int slot = 128 * c + 2 * lane;
+        CHECK(slot + 1 < X_SLOTS, "quarter poll");
+        for (int e = 0; e < 4; ++e) {
+          CHECK(2 * slot + e == 256 * c + 4 * lane + e, "quarter vin index");
+          got[2 * slot + e]++;
+        }
+      }
+    for (int r = 0; r < HIDDEN; ++r) CHECK(got[r] == 1, "quarter value %d", r);
   }
 
-  // lm_head rows: [0, VOCAB) exactly once over (w, c, chunk, i)
+  // ---- gate/up rows, INT slots, down input order ----
+  {
+    std::vector<int> g(INTER, 0);
+    for (int x = 0; x < NXCD; ++x)
+      for (int i = 0; i < NLOC; ++i)
+        for (int m = 0; m < LINES_GU; ++m) {
+          const bool up = m >= 2 * GU_PER_WG;
+          const int mm = up ? m - 2 * GU_PER_WG : m;
+          const int row = ICOLS * x + GU_PER_WG * i + (mm >> 1);
+          CHECK(row < INTER, "gu row");
+          if (!up && (mm & 1) == 0) g[row]++;
+        }
+    for (int r = 0; r < INTER; ++r) CHECK(g[r] == 1, "gate row %d", r);
+    // compute wave c: gate rows 3c + jj at lines 2(3c + jj), up at 24 + 2(3c + jj)
+    for (int c = 0; c < NCW; ++c)
+      for (int jj = 0; jj < 3; ++jj) CHECK(2 * GU_PER_WG + 2 * (3 * c + jj) + 1 < LINES_GU, "gu lines");
+    // INT slots and the down poll: pair k = 32 c + lane -> values 12 (k/4) + 3 (k%4) + {0,1,2}
+    std::vector<int> seen(ICOLS, 0);
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < 32; ++lane) {
+        const int k = 32 * c + lane, slot = 64 * c + 2 * lane;
+        CHECK(slot == int_slot(k >> 2, k & 3, 0) && slot + 1 == int_slot(k >> 2, k & 3, 1), "int slots");
+        CHECK(slot + 1 < INT_SLOTS, "int range");
+        for (int e = 0; e < 3; ++e) seen[GU_PER_WG * (k >> 2) + 3 * (k & 3) + e]++;
+      }
+    for (int e = 0; e < ICOLS; ++e) CHECK(seen[e] == 1, "inter value %d", e);
+    // down ring lines: row 32 i + m, columns 384 x + 8 ln (ln < 48)
+    std::vector<int> rows(HIDDEN * NXCD, 0);
+    for (int x = 0; x < NXCD; ++x)
+      for (int i = 0; i < NLOC; ++i)
+        for (int m = 0; m < LINES_DOWN; ++m)
+          for (int lane = 0; lane < WAVE; ++lane) {
+            const int ln = lane < 48 ? lane : lane - 48;
+            const int row = HROWS * i + m, col = ICOLS * x + 8 * ln;
+            CHECK(row < HIDDEN && col >= ICOLS * x && col + 8 <= ICOLS * (x + 1), "down line");
+            if (lane == 0) rows[x * HIDDEN + row]++;
+          }
+    for (int r = 0; r < HIDDEN * NXCD; ++r) CHECK(rows[r] == 1, "down row %d", r);
+  }
+
+  // ---- ring schedule: every stage fits the ring ----
+  for (int ctx = 1; ctx <= MAX_SEQ_LIMIT; ++ctx)
+    for (int s = 0; s < NSPLIT; ++s)
+      for (int st = 0; st < NSTAGE; ++st) CHECK(stage_lines(st, ctx, s) <= RING_LINES, "stage lines");
+
+  // ---- lm_head rows: [0, VOCAB) exactly once over (w, v, k, j) ----
   {
     std::vector<int> seen(VOCAB, 0);
     CHECK(lm_row0(NWG - 1) + lm_rows(NWG - 1) == VOCAB, "lm rows end");
+    CHECK(LM_ITERS % 2 == 0, "two-buffer lm loop needs an even iteration count");
     for (int w = 0; w < NWG; ++w) {
       CHECK(lm_rows(w) <= LM_MAX_ROWS, "lm rows");
-      for (int m = 0; m < NGW; ++m)
-        for (int k = 0; k < LM_CHUNKS; ++k)
-          for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i) {
-            int lr = lm_local_row(m, k, i);
+      for (int v = 0; v < NCW + NLW; ++v)
+        for (int k = 0; k < LM_ITERS; ++k)
+          for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) {
+            const int lr = lm_local_row(v, k, j);
             if (lr < lm_rows(w)) seen[lm_row0(w) + lr]++;
           }
     }
     for (int r = 0; r < VOCAB; ++r) CHECK(seen[r] == 1, "lm row %d seen %d", r, seen[r]);
+    // ARG: workgroup w stores slots 2w, 2w + 1; quarter c polls pairs 64 c + lane
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < WAVE; ++lane) {
+        const int slot = 128 * c + 2 * lane;
+        CHECK(slot == 2 * (64 * c + lane) && slot + 1 < ARG_SLOTS, "arg poll");
+      }
   }
 
-  // tags: distinct per (layer, stage id) and never the ARG tag; 24-bit epochs fit
+  // ---- tags: distinct per (layer, stage), never the ARG tag, epoch >= 1 never 0 ----
   {
     std::vector<int> seen(256, 0);
     for (int l = 0; l < MAX_LAYERS; ++l)
-      for (int sid = 0; sid <= SID_X; ++sid) seen[tag_of(0, l, sid)]++;
+      for (int st = 0; st < NSTAGE; ++st) seen[tag_of(0, l, st)]++;
     seen[tag_arg(0)]++;
-    for (int i = 0; i < 256; ++i) CHECK(seen[i] <= 1, "tag collision %d", i);
+    for (int e = 0; e < 256; ++e) CHECK(seen[e] <= 1, "tag collision %d", e);
     CHECK(tag_of(1, 0, 0) != 0 && tag_arg(1) != 0, "tags of epoch >= 1 are never 0");
-    CHECK((tag_of((1u << 24) - 1, 27, SID_X) >> 8) == (1u << 24) - 1, "24-bit epoch");
   }
-
-  // stage sequence: fin non-decreasing, +1 steps, LMH chunks share one fin; types cycle
-  for (int mode = 0; mode < 3; ++mode)
-    for (int L = 1; L <= MAX_LAYERS; ++L) {
-      if (mode != MODE_DECODE && L != 1) continue;
-      const int steps = 3, total = stages_per_token(mode, L) * steps;
-      int prev_fin = -1, nfin = 0;
-      for (int i = 0; i < total; ++i) {
-        StageDesc d = stage_desc(mode, L, i);
-        CHECK(d.token == i / stages_per_token(mode, L), "token");
-        CHECK(d.fin == prev_fin || d.fin == prev_fin + 1, "fin step mode%d L%d i%d", mode, L, i);
-        if (d.fin != prev_fin) ++nfin;
-        prev_fin = d.fin;
-        CHECK(d.layer >= 0 && d.layer < L, "layer");
-        CHECK(d.chunk >= 0 && d.chunk < LM_CHUNKS, "chunk");
-        if (mode == MODE_DECODE && d.type != C_LMH) CHECK(d.type == (i % stages_per_token(mode, L)) % 5, "type order");
-      }
-      CHECK(nfin == fins_per_token(mode, L) * steps, "fin count mode%d L%d", mode, L);
-    }
 
   if (g_fail) {
     fprintf(stderr, "layout_check: %d failures\n", g_fail);

@@ -3,21 +3,27 @@
 // tied lm_head, argmax) and, in generate mode, feeds each argmax back as the
 // next step's input without returning to the host.
 //
-// Design (measured on MI355X before it was written):
-//  * one 576-thread workgroup per CU (256), fixed work partition (qwen_layout.h);
-//  * no grid barrier: every inter-workgroup hand-off is an exchange buffer of
-//    8-byte slots carrying payload + step tag, written with device-scope (sc1)
-//    stores and polled with device-scope loads. A release/acquire grid barrier
-//    measured 8.3 us per crossing on this part; a tagged-slot hand-off costs
-//    one store->load visibility latency (~0.6 us);
-//  * wave specialisation: waves 0-7 stream weights with nontemporal 16-B loads
-//    issued two stages ahead into registers; wave 8 (the exchange wave) polls
-//    the next stage's input, applies the vector work (RMSNorm, q/k norm, RoPE,
-//    KV-cache write, split-K softmax merge, argmax) and hands it over in LDS.
-//    Loads retire in order per wave, so polling from a weight-streaming wave
-//    would wait behind its own prefetches; a separate wave does not;
-//  * inside a workgroup, the 8 compute waves meet through LDS counters (last
-//    arriver finalises), never s_barrier, so the exchange wave runs free;
+// Design (from measurements on MI355X):
+//  * one 512-thread workgroup per CU; workgroup w runs on XCD w % 8, and the
+//    work partition (qwen_layout.h) keeps each kv head's QKV rows, attention
+//    splits, softmax combine, o_proj and a 384-row slice of the MLP inside one
+//    XCD. Per layer only two steps cross XCDs: the sums of the 8 per-XCD
+//    o_proj and down partials into the residual stream (each workgroup reads
+//    its 32 rows from the 8 XCDs);
+//  * no grid barrier: every hand-off is an exchange buffer of 8-byte slots
+//    carrying payload + step tag, written with device-scope stores and polled
+//    with device-scope loads (one-way latency 0.3-0.5 us; a fence-based flag
+//    costs 1-2 us more);
+//  * waves 0-3 compute: each polls a quarter of a stage's input, the quarters
+//    meet in LDS, and each wave computes a quarter of the stage's rows and
+//    stores its own results. They hold no outstanding weight loads, so a poll
+//    never waits behind a prefetch;
+//  * waves 4-7 stream every stage's weights and K/V rows with LDS-DMA
+//    (global_load_lds_dwordx4) into a 128 KB ring of 1 KB lines, up to 128
+//    lines ahead of the compute waves; in the lm_head they compute rows
+//    alongside the compute waves;
+//  * the residual stream stays fp32 inside the workgroup that owns its rows;
+//    only the all-gathered copies are fp16;
 //  * every wait is bounded by a wall-clock deadline; a missed deadline sets a
 //    status word and all waves leave, so a broken exchange cannot hang the GPU.
 //
@@ -41,7 +47,6 @@ using namespace ql;
 typedef unsigned int u32;
 typedef unsigned long long u64;
 typedef u32 v4u __attribute__((ext_vector_type(4)));
-typedef u32 v2u __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -49,17 +54,16 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 constexpr float RMS_EPS = 1e-6f;
 constexpr u32 ST_TIMEOUT = 1u;
 constexpr u32 ST_BAD_TOKEN = 2u;
-// optional device timestamps (wall clock) per workgroup and finalised stage of one token
-constexpr int TRACE_EVENTS = 8;
+constexpr int DMA_DEPTH = 16;  // LDS-DMA lines a loader wave keeps in flight
+// optional device timestamps (wall clock) per workgroup and stage of one token
+constexpr int TRACE_EVENTS = 4;
 enum TraceEvent : int {
-  TR_POLL = 0,     // exchange wave starts waiting for the stage input
-  TR_PUBLISH = 1,  // stage input handed to the compute waves
-  TR_FINAL = 2,    // stage results stored
-  TR_COMBINE = 3,  // attention merge stored / argmax known
-  TR_CSTART = 4,   // compute wave 0 of the stage's group saw the input
-  TR_CDONE = 5,    // compute wave 0 of the stage's group finished the stage
-  TR_FSTART = 6,   // the finalising wave starts finalising
+  TR_POLL = 0,   // compute wave 0 starts waiting for the stage input
+  TR_INPUT = 1,  // compute wave 0 has its quarter of the input
+  TR_SYNC = 2,   // compute wave 0 passed the compute-wave barrier (whole input in LDS)
+  TR_STORE = 3,  // compute wave 0 stored its results
 };
+QL_HD int trace_stages(int L) { return NSTAGE * L + 1; }
 
 struct KParams {
   const _Float16* embed;
@@ -70,18 +74,18 @@ struct KParams {
   const _Float16* sin_t;
   _Float16* k_cache;
   _Float16* v_cache;
-  _Float16* hidden_out;  // [1024] fp16
-  float* norm_out;       // [1024] fp32
-  int* out_tokens;       // [num_steps]
-  const int* forced;     // nullable [num_steps]
-  float* logits_out;     // nullable [num_steps][VOCAB]
-  float* hidden_steps;   // nullable [num_steps][HIDDEN]
+  _Float16* hidden_out;    // [1024] fp16
+  float* norm_out;         // [1024] fp32
+  int* out_tokens;         // [num_steps]
+  const int* forced;       // nullable [num_steps]
+  float* logits_out;       // nullable [num_steps][VOCAB]
+  float* hidden_steps;     // nullable [num_steps][HIDDEN]
   const _Float16* in_vec;  // MODE_LMHEAD / MODE_MLP input [1024]
   float* out_vec;          // MODE_MLP output [1024]
   u64* ws;                 // exchange slots
   u32* status;             // status word (device scope)
   u64 deadline;            // wall-clock ticks a single wait may take
-  u64* trace;              // nullable [NWG][fins per token][TRACE_EVENTS]
+  u64* trace;              // nullable [NWG][trace_stages(L)][TRACE_EVENTS]
   int trace_token;         // token index whose stages are traced
   int mode, num_layers, first_token, start_pos, num_steps, max_seq;
   float attn_scale;
@@ -91,21 +95,19 @@ struct KParams {
 // ------------------------------------------------------------------------------------
 // small device helpers
 
-__device__ __forceinline__ v4u ld_nt(const _Float16* p) { return __builtin_nontemporal_load((const v4u*)p); }
-__device__ __forceinline__ v4u ld_plain(const _Float16* p) { return *(const v4u*)p; }
+__device__ __forceinline__ v4u ld_nt(const void* p) { return __builtin_nontemporal_load((const v4u*)p); }
 
-__device__ __forceinline__ float dot8(v4u w, const float* a) {
+// 8 fp16 weights (one 16-byte load) dotted with 8 fp32 activations
+__device__ __forceinline__ float dot8(v4u w, const float (&a)[8]) {
   h8 h = __builtin_bit_cast(h8, w);
-  float4 a0 = *(const float4*)a;
-  float4 a1 = *(const float4*)(a + 4);
-  float s = (float)h[0] * a0.x;
-  s = fmaf((float)h[1], a0.y, s);
-  s = fmaf((float)h[2], a0.z, s);
-  s = fmaf((float)h[3], a0.w, s);
-  s = fmaf((float)h[4], a1.x, s);
-  s = fmaf((float)h[5], a1.y, s);
-  s = fmaf((float)h[6], a1.z, s);
-  s = fmaf((float)h[7], a1.w, s);
+  float s = (float)h[0] * a[0];
+  s = fmaf((float)h[1], a[1], s);
+  s = fmaf((float)h[2], a[2], s);
+  s = fmaf((float)h[3], a[3], s);
+  s = fmaf((float)h[4], a[4], s);
+  s = fmaf((float)h[5], a[5], s);
+  s = fmaf((float)h[6], a[6], s);
+  s = fmaf((float)h[7], a[7], s);
   return s;
 }
 
@@ -181,6 +183,13 @@ __device__ __forceinline__ void reduce6(const float (&v)[6], float& p, float& q)
   p = row16_sum(pack16(x1, x2));
   q = row16_sum(pack16(x3, x3));
 }
+// 8 row partials -> full sums: y0 rows 0..3 = (v0, v2, v1, v3), y1 rows 0..3 = (v4, v6, v5, v7)
+__device__ __forceinline__ void reduce8(const float (&v)[8], float& y0, float& y1) {
+  y0 = row16_sum(pack16(pack32(v[0], v[1]), pack32(v[2], v[3])));
+  y1 = row16_sum(pack16(pack32(v[4], v[5]), pack32(v[6], v[7])));
+}
+// row (0..7 of reduce8's inputs) whose total lane `lane` holds in y0; y1 holds row + 4
+__device__ __forceinline__ int reduce8_row(int lane) { return (lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : (lane >> 4)); }
 // (value, index) arg-max over the whole wave, lowest index on ties; every lane gets the result
 __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) {
@@ -204,6 +213,9 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   i = (int)ri[0];
   better(v, i, __uint_as_float(rv[1]), (int)ri[1]);
 }
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 
 __device__ __forceinline__ u32 pack_h2(float a, float b) {
   h2 h = {(_Float16)a, (_Float16)b};
@@ -220,7 +232,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const u64* ws) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)ws, 0, 0x7fffffff, 0x00020000);
 }
 // one 16-byte device-scope (sc1) load of two slots at byte offset voff + soff
-// (voff per lane, soff wave-uniform so it travels in the instruction's soffset)
 __device__ __forceinline__ v4u ld_pair(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 16);
 }
@@ -234,68 +245,89 @@ __device__ __forceinline__ void lds_st(u32* p, u32 v) {
 __device__ __forceinline__ void lds_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local"); }
 __device__ __forceinline__ void lds_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local"); }
 
+// LDS-DMA: 16 bytes per lane from global memory to LDS byte address lds + 16 lane.
+// Issued through inline assembly so the compiler adds no vmcnt wait before the
+// wave's later LDS accesses; the loader tracks completion with explicit vmcnt waits.
+__device__ __forceinline__ void dma16(const void* g, u32 lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(lds), "v"(g) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // ------------------------------------------------------------------------------------
 // workgroup shared state
 
 struct Shared {
-  float in[2][INTER];            // stage input prepared by the exchange wave (parity of fin)
-  float red[2][NCW * 260];       // per-wave partial results (parity of fin)
-  float xres[HID_PER_WG];        // residual rows before attention (fp32)
-  float actres[HID_PER_WG];      // residual rows after attention (fp32)
-  u32 ready;                     // fin + 1 of the newest prepared input
-  u32 cnt[2];                    // compute-wave arrivals at the current fin of each parity
-  u32 done[2];                   // fin + 1 of the newest finalised fin of each parity
+  v4u ring[RING_LINES][LINE_BYTES / 16];  // 128 KB weight / K-V line ring (must stay first: LDS offset 0)
+  float vin[2][HIDDEN];            // stage input (fp32), alternating between stages
+  float red[2][NCW];               // per-wave partial sums of squares, alternating
+  float qr[4 * HD];                // roped q (2 heads), roped k, v of the current position
+  float apart[NCW][2][PART_PER_HEAD];  // per-wave attention partials (m, l, acc)
+  float opart[2][NXCD][HROWS];     // per-XCD partial rows for the residual sums, alternating
+  float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32)
+  float actres[HROWS];             // fp32 post-attention residual, same rows
+  float xfin[HIDDEN];              // lm_head input (fp32)
+  float lmv[NCW + NLW];            // per-wave lm_head best value
+  int lmi[NCW + NLW];              // per-wave lm_head best row
+  float argv[NCW];                 // per-wave best of the global argmax
+  int argi[NCW];
+  u32 sync;                        // compute-wave barrier arrivals (monotonic)
+  u32 done_upto[NLW];              // loader wave q: smallest line (== q mod 4) not yet in the ring
+  u32 cons[NCW];                   // compute wave c: ring lines below this are no longer read
+  u32 xfin_cnt;                    // quarters of xfin stored (monotonic)
+  u32 lm_cnt;                      // lm_head partials stored (monotonic)
   u32 abort;
+  // the layer pointer table, copied from global memory at start: reading it from
+  // LDS keeps the loader waves' vmcnt free of anything but their own DMAs
+  LDGLayerWeight lw[MAX_LAYERS];
 };
 
-// ------------------------------------------------------------------------------------
-// exchange-wave polling
-
-struct Poll {
-  __amdgpu_buffer_rsrc_t r;
+struct Ctl {
   const KParams* P;
   Shared* S;
+  __amdgpu_buffer_rsrc_t r;
   bool ok;
+  u64 deadline;
 };
 
-__device__ __forceinline__ bool poll_give_up(Poll& pl, u64 t0, int& spins) {
+__device__ __forceinline__ bool give_up(Ctl& C, u64 t0, int& spins) {
   ++spins;
-  if ((spins & 15) == 0 && wall_clock64() - t0 > pl.P->deadline) {
-    __hip_atomic_fetch_or(pl.P->status, ST_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
+  if ((spins & 15) == 0) {
+    if (lds_ld(&C.S->abort)) return true;
+    if (wall_clock64() - t0 > C.deadline) {
+      __hip_atomic_fetch_or(C.P->status, ST_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      lds_st(&C.S->abort, 1u);
+      return true;
+    }
   }
-  if ((spins & 255) == 0) {
-    if (__hip_atomic_load(pl.P->status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return true;
+  if ((spins & 255) == 0 && __hip_atomic_load(C.P->status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+    lds_st(&C.S->abort, 1u);
+    return true;
   }
   return false;
 }
 
-__device__ __forceinline__ void xtrace(const KParams& P, int token, u32 fin_in_token, int what) {
-  if (P.trace && token == P.trace_token && __lane_id() == 0) {
-    const int FT = fins_per_token(P.mode, P.num_layers);
-    P.trace[((long)blockIdx.x * FT + fin_in_token) * TRACE_EVENTS + what] = wall_clock64();
-  }
-}
-
 // Polls K slot pairs per lane until both slots of every pair carry `tag`. Pair k
-// of this lane starts at byte voff + soff_of(k) of the workspace; soff_of(k) must be
-// wave-uniform. Lanes with active == false take no part.
-template <int K, typename F>
-__device__ __forceinline__ void poll_pairs(Poll& pl, u32 tag, int voff, bool active, F soff_of, v4u (&out)[K]) {
-  if (!pl.ok) return;
+// of this lane is at byte voff[k] + soff of the workspace (soff wave-uniform).
+// Lanes with active == false take no part.
+template <int K>
+__device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int soff, bool active, v4u (&out)[K]) {
   bool done[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     done[k] = !active;
     out[k] = v4u{0, 0, 0, 0};
   }
+  if (!C.ok) return;
   const u64 t0 = wall_clock64();
   int spins = 0;
   for (;;) {
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      if (!done[k]) out[k] = ld_pair(pl.r, voff, soff_of(k));
+      if (!done[k]) out[k] = ld_pair(C.r, voff[k], soff);
     bool all = true;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -303,22 +335,26 @@ __device__ __forceinline__ void poll_pairs(Poll& pl, u32 tag, int voff, bool act
       all = all && done[k];
     }
     if (__all(all)) return;
-    if (poll_give_up(pl, t0, spins)) {
-      pl.ok = false;
+    if (give_up(C, t0, spins)) {
+      C.ok = false;
       return;
     }
     __builtin_amdgcn_s_sleep(1);
   }
 }
 
-// exchange wave: wait until fin - 2 (same parity) is finalised, so in[fin % 2] is free
-__device__ __forceinline__ void wait_consumed(Poll& pl, u32 fin) {
-  if (!pl.ok || fin < 2) return;
+// spins until *p >= v (LDS), bounded
+__device__ __forceinline__ void lds_wait_ge(Ctl& C, const u32* p, u32 v) {
+  if (!C.ok) return;
+  if (lds_ld(p) >= v) {
+    lds_acquire();
+    return;
+  }
   const u64 t0 = wall_clock64();
   int spins = 0;
-  while (lds_ld(&pl.S->done[fin & 1]) < fin - 1) {
-    if (poll_give_up(pl, t0, spins)) {
-      pl.ok = false;
+  while (lds_ld(p) < v) {
+    if (give_up(C, t0, spins)) {
+      C.ok = false;
       return;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -326,848 +362,910 @@ __device__ __forceinline__ void wait_consumed(Poll& pl, u32 fin) {
   lds_acquire();
 }
 
-__device__ __forceinline__ void publish(Poll& pl, u32 fin) {
-  lds_release();
-  if (__lane_id() == 0) lds_st(&pl.S->ready, fin + 1);
+__device__ __forceinline__ void trace_ev(const KParams& P, int token, int stage, int what) {
+  if (P.trace && token == P.trace_token && __lane_id() == 0)
+    P.trace[((long)blockIdx.x * trace_stages(P.num_layers) + stage) * TRACE_EVENTS + what] = wall_clock64();
 }
 
-// RMS of the 16 values a lane holds as x[4(lane + 64 i) + j], i < 4, j < 4
-__device__ __forceinline__ float rstd_1024(const float (&x)[16]) {
-  float ss = 0.f;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) ss = fmaf(x[k], x[k], ss);
-  ss = wave_sum(ss);
-  return rsqrtf(ss * (1.0f / HIDDEN) + RMS_EPS);
-}
-
-// polls a 1024-value H2 vector (512 slots from slot `base`) into x[4(lane + 64 i) + j]
-__device__ __forceinline__ void poll_vec1024(Poll& pl, u32 tag, long base, float (&x)[16]) {
-  v4u v[4];
-  const int lane = __lane_id();
-  poll_pairs<4>(pl, tag, lin_voff(lane), true, [&](int k) -> int { return (int)lin_soff(base, k); }, v);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    x[4 * k + 0] = lo_h(v[k].x);
-    x[4 * k + 1] = hi_h(v[k].x);
-    x[4 * k + 2] = lo_h(v[k].z);
-    x[4 * k + 3] = hi_h(v[k].z);
-  }
-}
-
-// the lane's 16 norm weights w[4(lane + 64k) + j]; loaded before polling so the
-// load overlaps the wait instead of following it
-struct NormW {
-  h4 v[4];
-};
-__device__ __forceinline__ NormW load_norm(const _Float16* w) {
-  NormW n;
-  const int lane = __lane_id();
-#pragma unroll
-  for (int k = 0; k < 4; ++k) n.v[k] = *(const h4*)(w + 4 * (lane + 64 * k));
-  return n;
-}
-// in[i] = x[i] * rstd * w[i] for the lane's 16 values
-__device__ __forceinline__ void store_normed(float* dst, const float (&x)[16], float rstd, const NormW& wv) {
-  const int lane = __lane_id();
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = 4 * (lane + 64 * k);
-    float4 o = make_float4(x[4 * k] * rstd * (float)wv.v[k][0], x[4 * k + 1] * rstd * (float)wv.v[k][1],
-                           x[4 * k + 2] * rstd * (float)wv.v[k][2], x[4 * k + 3] * rstd * (float)wv.v[k][3]);
-    *(float4*)(dst + i) = o;
-  }
-}
+__device__ __forceinline__ const v4u* ring_line(Shared* S, u32 n) { return S->ring[n % RING_LINES]; }
 
 // ------------------------------------------------------------------------------------
-// exchange wave program
+// lm_head rows (every wave): rows [lm_row0(w), +lm_rows(w)) of the tied embedding,
+// 8 rows per wave per iteration, register double-buffered, dotted with xfin (fp32)
 
-__device__ void exchange_wave(const KParams& P, Shared* S) {
-  const int w = blockIdx.x;
+__device__ __forceinline__ void lm_issue(const KParams& P, int v, int k, int r0, int nr, v4u (&buf)[16]) {
   const int lane = __lane_id();
-  Poll pl{ws_rsrc(P.ws), &P, S, true};
-  const int L = P.num_layers;
-  const int FT = fins_per_token(P.mode, L);
-
-  if (P.mode == MODE_MLP) {
-    const LDGLayerWeight& lw = P.layers[0];
-    // GU input: x -> RMSNorm * post_norm; residual rows x[4w..4w+3]
-    float x[16];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      h4 v = *(const h4*)(P.in_vec + 4 * (lane + 64 * k));
-      for (int j = 0; j < 4; ++j) x[4 * k + j] = (float)v[j];
-    }
-    const float rs = rstd_1024(x);
-    store_normed(S->in[0], x, rs, load_norm((const _Float16*)lw.post_attn_layernorm_weight));
-    if (lane < HID_PER_WG) S->actres[lane] = (float)P.in_vec[HID_PER_WG * w + lane];
-    publish(pl, 0);
-    // DOWN input: SiLU(gate)*up from every workgroup
-    wait_consumed(pl, 1);
-    v4u v[12];
-    poll_pairs<12>(pl, tag_of(P.epoch0, 0, SID_INT), lin_voff(lane), true,
-                   [&](int k) -> int { return (int)lin_soff(slot_int(0, 0), k); }, v);
-    if (!pl.ok) { S->abort = 1; return; }
-#pragma unroll
-    for (int k = 0; k < 12; ++k) {
-      const int i = 4 * (lane + 64 * k);
-      *(float4*)(S->in[1] + i) = make_float4(lo_h(v[k].x), hi_h(v[k].x), lo_h(v[k].z), hi_h(v[k].z));
-    }
-    publish(pl, 1);
-    return;
+  for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) {
+    int lr = lm_local_row(v, k, j);
+    if (lr >= nr) lr = nr - 1;  // clamped rows are loaded but not used
+    const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
+    buf[2 * j] = ld_nt(base + 8 * lane);
+    buf[2 * j + 1] = ld_nt(base + 512 + 8 * lane);
   }
+}
 
-  if (P.mode == MODE_LMHEAD) {
-    float x[16];
+__device__ __forceinline__ void lm_consume(const KParams& P, int v, int k, int r0, int nr, int t, const v4u (&buf)[16],
+                                           const float (&a)[8], const float (&b)[8], float& best, int& bidx) {
+  const int lane = __lane_id();
+  float part[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      h4 v = *(const h4*)(P.in_vec + 4 * (lane + 64 * k));
-      for (int j = 0; j < 4; ++j) x[4 * k + j] = (float)v[j];
-    }
+  for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) part[j] = dot8(buf[2 * j], a) + dot8(buf[2 * j + 1], b);
+  float y0, y1;
+  reduce8(part, y0, y1);
+  // lanes 0, 16, 32, 48 hold rows (0, 4), (2, 6), (1, 5), (3, 7): each lane's rows ascend
+  // over the token, so a strict > keeps the lowest index among equal logits
+  if ((lane & 15) == 0) {
+    const int jr = reduce8_row(lane);
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      *(float4*)(S->in[0] + 4 * (lane + 64 * k)) = make_float4(x[4 * k], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
-    publish(pl, 0);
-  }
-
-  int token = P.first_token;
-  for (int t = 0; t < P.num_steps; ++t) {
-    const u32 epoch = P.epoch0 + (u32)t;
-    const int pos = P.start_pos + t;
-    if (P.mode == MODE_DECODE) {
-      const int ctx = pos + 1;
-      for (int l = 0; l < L; ++l) {
-        const LDGLayerWeight& lw = P.layers[l];
-        const int par = l & 1;
-        u32 fin = (u32)(t * FT + 5 * l);
-        // ---- QKV input: residual stream -> RMSNorm * input_layernorm
-        wait_consumed(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-        const NormW w_in = load_norm((const _Float16*)lw.input_layernorm_weight);
-        float x[16];
-        if (l == 0) {
-          const _Float16* row = P.embed + (long)token * HIDDEN;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            h4 v = *(const h4*)(row + 4 * (lane + 64 * k));
-            for (int j = 0; j < 4; ++j) x[4 * k + j] = (float)v[j];
-          }
-          if (lane < HID_PER_WG) S->xres[lane] = (float)row[HID_PER_WG * w + lane];
-        } else {
-          poll_vec1024(pl, tag_of(epoch, l - 1, SID_X), slot_x(par, 0), x);
+    for (int h = 0; h < 2; ++h) {
+      const int lr = lm_local_row(v, k, jr + 4 * h);
+      const float val = h == 0 ? y0 : y1;
+      if (lr < nr) {
+        if (P.logits_out) P.logits_out[(long)t * VOCAB + r0 + lr] = val;
+        const float vv = __builtin_isnan(val) ? -INFINITY : val;
+        if (vv > best) {
+          best = vv;
+          bidx = r0 + lr;
         }
-        if (!pl.ok) break;
-        {
-          const float rs = rstd_1024(x);
-          store_normed(S->in[fin & 1], x, rs, w_in);
-        }
-        publish(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-
-        // ---- attention input: raw q (2 heads), k, v of kv head g -> norms, RoPE, KV write
-        ++fin;
-        wait_consumed(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-        const int g = att_kv(w), s = att_split(w);
-        {
-          const int d0 = 4 * (lane & 31);
-          const h4 cv = *(const h4*)(P.cos_t + (long)pos * HD + d0);
-          const h4 sv = *(const h4*)(P.sin_t + (long)pos * HD + d0);
-          const h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d0);
-          const h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d0);
-          v4u vq[1], vkv[1];
-          // q slots 128g + 2 lane; k slots (lane < 32) or v slots (lane >= 32)
-          poll_pairs<1>(pl, tag_of(epoch, l, SID_QKV), attq_voff(lane), true,
-                        [&](int) -> int { return (int)attq_soff(par, g); }, vq);
-          poll_pairs<1>(pl, tag_of(epoch, l, SID_QKV), attkv_voff(lane), true,
-                        [&](int) -> int { return (int)attkv_soff(par, g); }, vkv);
-          if (!pl.ok) break;
-          // vq: q values 4 lane .. (q head 2g for lane < 32, 2g+1 above)
-          // vkv: lane < 32: k dims 4 lane.., lane >= 32: v dims 4(lane-32)..
-          float q[4] = {lo_h(vq[0].x), hi_h(vq[0].x), lo_h(vq[0].z), hi_h(vq[0].z)};
-          float kv[4] = {lo_h(vkv[0].x), hi_h(vkv[0].x), lo_h(vkv[0].z), hi_h(vkv[0].z)};
-          // q head norms (each 32-lane half is one head)
-          float ssq = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
-          ssq = half_sum(ssq);
-          const float rq = rsqrtf(ssq * (1.0f / HD) + RMS_EPS);
-          float ssk = kv[0] * kv[0] + kv[1] * kv[1] + kv[2] * kv[2] + kv[3] * kv[3];
-          ssk = half_sum(ssk);  // lanes < 32: k norm; lanes >= 32: unused (v)
-          const float rk = rsqrtf(ssk * (1.0f / HD) + RMS_EPS);
-          float qq[4], kk[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            qq[j] = q[j] * rq * (float)qn[j];
-            kk[j] = kv[j] * rk * (float)kn[j];
-          }
-          // rotate-half RoPE: partner dims d +- 64 live in lane ^ 16
-          const bool lo_half = (lane & 31) < 16;
-          float qo[4], ko[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float qp = xor16(qq[j]);
-            const float kp = xor16(kk[j]);
-            const float c = (float)cv[j], sgn = lo_half ? -(float)sv[j] : (float)sv[j];
-            qo[j] = qq[j] * c + qp * sgn;
-            ko[j] = kk[j] * c + kp * sgn;
-          }
-          float* in = S->in[fin & 1];
-          *(float4*)(in + 4 * lane) = make_float4(qo[0], qo[1], qo[2], qo[3]);  // q0r | q1r
-          if (lane < 32)
-            *(float4*)(in + 256 + 4 * lane) = make_float4(ko[0], ko[1], ko[2], ko[3]);  // kr
-          else
-            *(float4*)(in + 384 + 4 * (lane - 32)) = make_float4(kv[0], kv[1], kv[2], kv[3]);  // vr
-          // the split holding `pos` writes this position's K (roped) and V to the cache
-          if (att_t0(ctx, s) <= pos && pos < att_t1(ctx, s)) {
-            const long row = (((long)l * NKV + g) * P.max_seq + pos) * HD;
-            if (lane < 32) {
-              h4 o = {(_Float16)ko[0], (_Float16)ko[1], (_Float16)ko[2], (_Float16)ko[3]};
-              __hip_atomic_store((u64*)(P.k_cache + row + d0), __builtin_bit_cast(u64, o), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-              h4 o = {(_Float16)kv[0], (_Float16)kv[1], (_Float16)kv[2], (_Float16)kv[3]};
-              __hip_atomic_store((u64*)(P.v_cache + row + d0), __builtin_bit_cast(u64, o), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-            }
-          }
-        }
-        publish(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-
-        // ---- combine: q head w/16, dims [d0, d0+8) over the 32 splits of its kv head
-        {
-          const int h = cmb_head(w), gh = h / 2, ih = h % 2, d0 = cmb_d0(w);
-          v4u v[5];
-          // lane s < 32 reads split s: (m, l) and acc[d0 .. d0+8)
-          poll_pairs<5>(pl, tag_of(epoch, l, SID_PART), lane < NSPLIT ? cmb_voff(lane) : 0, lane < NSPLIT,
-                        [&](int k) -> int { return (int)cmb_soff(par, h, d0, k); }, v);
-          if (!pl.ok) break;
-          float m = -INFINITY, lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-          if (lane < NSPLIT) {
-            m = __uint_as_float(v[0].x);
-            lsum = __uint_as_float(v[0].z);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              acc[2 * k] = __uint_as_float(v[k + 1].x);
-              acc[2 * k + 1] = __uint_as_float(v[k + 1].z);
-            }
-          }
-          const float M = max16x(row16_max(m));  // over lanes 0-31 (lanes >= 32 hold -inf)
-          const float e = (lane < NSPLIT && m != -INFINITY) ? __expf(m - M) : 0.f;
-          float Lt = half_sum(e * lsum);
-          float o[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) o[j] = half_sum(e * acc[j]);
-          const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-          // drain the KV-cache stores before any workgroup can depend on this step
-          __builtin_amdgcn_s_waitcnt(0);
-          // lane k < 4 stores dims 2k, 2k+1 (static selects: no lane-indexed array)
-          const float oa = lane == 0 ? o[0] : (lane == 1 ? o[2] : (lane == 2 ? o[4] : o[6]));
-          const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
-          if (lane < 4)
-            ll_store(P.ws, slot_att(par, 4 * w + lane), pack_h2(oa * inv, ob * inv), tag_of(epoch, l, SID_ATT));
-          xtrace(P, t, fin - (u32)(t * FT), TR_COMBINE);
-        }
-
-        // ---- o_proj input: all 2048 attention values
-        ++fin;
-        wait_consumed(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-        {
-          v4u v[8];
-          poll_pairs<8>(pl, tag_of(epoch, l, SID_ATT), lin_voff(lane), true,
-                        [&](int k) -> int { return (int)lin_soff(slot_att(par, 0), k); }, v);
-          if (!pl.ok) break;
-          float* in = S->in[fin & 1];
-#pragma unroll
-          for (int k = 0; k < 8; ++k)
-            *(float4*)(in + 4 * (lane + 64 * k)) = make_float4(lo_h(v[k].x), hi_h(v[k].x), lo_h(v[k].z), hi_h(v[k].z));
-        }
-        publish(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-
-        // ---- gate/up input: post-attention residual -> RMSNorm * post_attention_layernorm
-        ++fin;
-        wait_consumed(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-        {
-          const NormW w_post = load_norm((const _Float16*)lw.post_attn_layernorm_weight);
-          poll_vec1024(pl, tag_of(epoch, l, SID_ACT), slot_act(par, 0), x);
-          if (!pl.ok) break;
-          const float rs = rstd_1024(x);
-          store_normed(S->in[fin & 1], x, rs, w_post);
-        }
-        publish(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-
-        // ---- down input: SiLU(gate)*up, 3072 values
-        ++fin;
-        wait_consumed(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-        {
-          v4u v[12];
-          poll_pairs<12>(pl, tag_of(epoch, l, SID_INT), lin_voff(lane), true,
-                         [&](int k) -> int { return (int)lin_soff(slot_int(par, 0), k); }, v);
-          if (!pl.ok) break;
-          float* in = S->in[fin & 1];
-#pragma unroll
-          for (int k = 0; k < 12; ++k)
-            *(float4*)(in + 4 * (lane + 64 * k)) = make_float4(lo_h(v[k].x), hi_h(v[k].x), lo_h(v[k].z), hi_h(v[k].z));
-        }
-        publish(pl, fin);
-        xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-      }
-      if (!pl.ok) break;
-
-      // ---- lm_head input: final residual -> RMSNorm * final_norm
-      const u32 fin = (u32)(t * FT + 5 * L);
-      wait_consumed(pl, fin);
-      xtrace(P, t, fin - (u32)(t * FT), TR_POLL);
-      const NormW w_fin = load_norm(P.final_norm);
-      float x[16];
-      poll_vec1024(pl, tag_of(epoch, L - 1, SID_X), slot_x(L & 1, 0), x);
-      if (!pl.ok) break;
-      const float rs = rstd_1024(x);
-      store_normed(S->in[fin & 1], x, rs, w_fin);
-      publish(pl, fin);
-      xtrace(P, t, fin - (u32)(t * FT), TR_PUBLISH);
-      if (w == 0) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int i = 4 * (lane + 64 * k);
-          h4 hv = {(_Float16)x[4 * k], (_Float16)x[4 * k + 1], (_Float16)x[4 * k + 2], (_Float16)x[4 * k + 3]};
-          *(h4*)(P.hidden_out + i) = hv;
-          const h4 wv = w_fin.v[k];
-          *(float4*)(P.norm_out + i) = make_float4(x[4 * k] * rs * (float)wv[0], x[4 * k + 1] * rs * (float)wv[1],
-                                                   x[4 * k + 2] * rs * (float)wv[2], x[4 * k + 3] * rs * (float)wv[3]);
-          if (P.hidden_steps)
-            *(float4*)(P.hidden_steps + (long)t * HIDDEN + i) = make_float4(x[4 * k], x[4 * k + 1], x[4 * k + 2], x[4 * k + 3]);
-        }
-      }
-    }
-
-    // ---- argmax over the 256 workgroup partials (lowest index on ties)
-    {
-      v4u v[4];
-      poll_pairs<4>(pl, tag_arg(epoch), lin_voff(lane), true,
-                    [&](int k) -> int { return (int)lin_soff(slot_arg(t & 1, 0), k); }, v);
-      if (!pl.ok) break;
-      float best = -INFINITY;
-      int bidx = 0x7fffffff;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float val = __uint_as_float(v[k].x);
-        const int idx = (int)v[k].z;
-        if (val > best || (val == best && idx < bidx)) {
-          best = val;
-          bidx = idx;
-        }
-      }
-      wave_argmax(best, bidx);
-      if (bidx < 0 || bidx >= VOCAB) bidx = 0;  // every logit NaN
-      if (w == 0 && lane == 0) P.out_tokens[t] = bidx;
-      xtrace(P, t, (u32)(FT - 1), TR_COMBINE);
-      token = (P.forced && t + 1 < P.num_steps) ? P.forced[t + 1] : bidx;
-      if (token < 0 || token >= VOCAB) {  // a forced id out of range: report and stop
-        __hip_atomic_fetch_or(P.status, ST_BAD_TOKEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pl.ok = false;
-        break;
       }
     }
   }
-  if (!pl.ok) lds_st(&S->abort, 1u);
+}
+
+__device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, u32 phase) {
+  Shared* S = C.S;
+  const int w = blockIdx.x, lane = __lane_id();
+  const int r0 = lm_row0(w), nr = lm_rows(w);
+  v4u A[16], B[16];
+  lm_issue(P, v, 0, r0, nr, A);
+  lds_wait_ge(C, &S->xfin_cnt, NCW * phase);
+  float a[8], b[8];
+  {
+    const float4 p0 = *(const float4*)(S->xfin + 8 * lane), p1 = *(const float4*)(S->xfin + 8 * lane + 4);
+    const float4 q0 = *(const float4*)(S->xfin + 512 + 8 * lane), q1 = *(const float4*)(S->xfin + 512 + 8 * lane + 4);
+    a[0] = p0.x; a[1] = p0.y; a[2] = p0.z; a[3] = p0.w; a[4] = p1.x; a[5] = p1.y; a[6] = p1.z; a[7] = p1.w;
+    b[0] = q0.x; b[1] = q0.y; b[2] = q0.z; b[3] = q0.w; b[4] = q1.x; b[5] = q1.y; b[6] = q1.z; b[7] = q1.w;
+  }
+  float best = -INFINITY;
+  int bidx = 0x7fffffff;
+  for (int k = 0; k < LM_ITERS; k += 2) {
+    lm_issue(P, v, k + 1, r0, nr, B);
+    lm_consume(P, v, k, r0, nr, t, A, a, b, best, bidx);
+    if (k + 2 < LM_ITERS) lm_issue(P, v, k + 2, r0, nr, A);
+    lm_consume(P, v, k + 1, r0, nr, t, B, a, b, best, bidx);
+  }
+  wave_argmax(best, bidx);
+  if (lane == 0) {
+    S->lmv[v] = best;
+    S->lmi[v] = bidx;
+  }
+  lds_release();
+  if (lane == 0) __hip_atomic_fetch_add(&S->lm_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // ------------------------------------------------------------------------------------
 // compute waves
 
-struct Buf {
-  v4u v[12];
+struct CW {
+  Ctl C;
+  int w, x, i, c, lane;
+  u32 nsync;   // barriers passed
+  int par_in;  // vin / red / opart buffer parity of the current stage
+  u32 gl;      // global ring line index of the next stage
 };
 
-__device__ __forceinline__ const LDGLayerWeight& layer_of(const KParams& P, int l) { return P.layers[l]; }
-
-// Issues stage d's weight (or KV-cache) loads for group member m into b. Every
-// path issues its loads unconditionally; rows outside the work range are
-// clamped to a valid row and ignored by the compute.
-__device__ __forceinline__ void prefetch(const KParams& P, const StageDesc& d, Buf& b, int w, int m, int lane) {
-  switch (d.type) {
-    case C_QKV: {
-      const LDGLayerWeight& lw = layer_of(P, d.layer);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = QKV_PER_WG * w + 4 * m + r;
-        const int mat = qkv_matrix(row);
-        const _Float16* base =
-            (const _Float16*)(mat == 0 ? lw.q_proj_weight : (mat == 1 ? lw.k_proj_weight : lw.v_proj_weight)) +
-            (long)qkv_row_in(row) * HIDDEN;
-        b.v[2 * r] = ld_nt(base + 8 * lane);
-        b.v[2 * r + 1] = ld_nt(base + 512 + 8 * lane);
-      }
-      break;
-    }
-    case C_ATT: {
-      const int pos = P.start_pos + d.token, ctx = pos + 1;
-      const int g = att_kv(w), s = att_split(w);
-      const int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s);
-      const int j = lane >> 4, q = lane & 15;
-#pragma unroll
-      for (int bb = 0; bb < 4; ++bb) {
-        int p = t0 + att_local_pos(m, j, bb);
-        if (!(p < t1 && p != pos)) p = 0;  // position 0 always exists; its value is unused
-        const long row = (((long)d.layer * NKV + g) * P.max_seq + p) * HD + 8 * q;
-        b.v[bb] = ld_plain(P.k_cache + row);
-        b.v[4 + bb] = ld_plain(P.v_cache + row);
-      }
-      break;
-    }
-    case C_OPROJ: {
-      const LDGLayerWeight& lw = layer_of(P, d.layer);
-      const _Float16* base = (const _Float16*)lw.o_proj_weight + (long)(HID_PER_WG * w + m) * QSZ;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) b.v[k] = ld_nt(base + 8 * lane + 512 * k);
-      break;
-    }
-    case C_GU: {
-      const LDGLayerWeight& lw = layer_of(P, d.layer);
-      // member 0,1: gate rows 6m..6m+5; member 2,3: up rows 6(m-2)..
-      const _Float16* mat = (const _Float16*)(m < 2 ? lw.gate_proj_weight : lw.up_proj_weight);
-#pragma unroll
-      for (int k = 0; k < 6; ++k) {
-        const _Float16* base = mat + (long)(INT_PER_WG * w + 6 * (m & 1) + k) * HIDDEN;
-        b.v[2 * k] = ld_nt(base + 8 * lane);
-        b.v[2 * k + 1] = ld_nt(base + 512 + 8 * lane);
-      }
-      break;
-    }
-    case C_DOWN: {
-      const LDGLayerWeight& lw = layer_of(P, d.layer);
-      const _Float16* base = (const _Float16*)lw.down_proj_weight + (long)(HID_PER_WG * w + m) * INTER;
-#pragma unroll
-      for (int k = 0; k < 6; ++k) b.v[k] = ld_nt(base + 8 * lane + 512 * k);
-      break;
-    }
-    default: {  // C_LMH
-      const int nrows = lm_rows(w), r0 = lm_row0(w);
-#pragma unroll
-      for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i) {
-        int lr = lm_local_row(m, d.chunk, i);
-        if (lr >= nrows) lr = nrows - 1;  // clamped rows are loaded but not used
-        const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
-        b.v[2 * i] = ld_nt(base + 8 * lane);
-        b.v[2 * i + 1] = ld_nt(base + 512 + 8 * lane);
-      }
-      break;
-    }
-  }
+// barrier of the 4 compute waves (monotonic LDS counter)
+__device__ __forceinline__ void sync4(CW& W) {
+  lds_release();
+  if (W.lane == 0) __hip_atomic_fetch_add(&W.C.S->sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  ++W.nsync;
+  lds_wait_ge(W.C, &W.C.S->sync, NCW * W.nsync);
 }
 
-struct CState {
-  float lm_best;
-  int lm_idx;
-};
-
-// returns false when the workgroup aborted
-__device__ __forceinline__ bool wait_ready(Shared* S, u32 fin, u64 deadline) {
-  if (lds_ld(&S->ready) > fin) {
+__device__ __forceinline__ u32 lines_done(const Shared* S) {
+  const u32 a = lds_ld(&S->done_upto[0]), b = lds_ld(&S->done_upto[1]);
+  const u32 c = lds_ld(&S->done_upto[2]), d = lds_ld(&S->done_upto[3]);
+  return min(min(a, b), min(c, d));
+}
+// waits until every ring line below `end` is in LDS
+__device__ __forceinline__ void wait_lines(CW& W, u32 end) {
+  if (!W.C.ok) return;
+  if (lines_done(W.C.S) >= end) {
     lds_acquire();
-    return true;
+    return;
   }
   const u64 t0 = wall_clock64();
   int spins = 0;
-  while (lds_ld(&S->ready) <= fin) {
-    if (lds_ld(&S->abort)) return false;
-    if ((++spins & 63) == 0 && wall_clock64() - t0 > deadline) return false;
+  while (lines_done(W.C.S) < end) {
+    if (give_up(W.C, t0, spins)) {
+      W.C.ok = false;
+      return;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   lds_acquire();
-  return true;
 }
-
-// One compute wave's arrival at finalised stage `fin`, which takes `n` arrivals;
-// returns true in the wave that arrives last: it finalises (and resets the counter).
-__device__ __forceinline__ bool arrive(Shared* S, u32 fin, u32 n) {
+// this wave no longer reads ring lines below `end`
+__device__ __forceinline__ void release_lines(CW& W, u32 end) {
   lds_release();
-  u32 old = 0;
-  if (__lane_id() == 0) old = __hip_atomic_fetch_add(&S->cnt[fin & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  old = __builtin_amdgcn_readfirstlane(old);
-  const bool last = old == n - 1;
-  if (last) {
-    lds_acquire();
-    if (__lane_id() == 0) lds_st(&S->cnt[fin & 1], 0u);
-  }
-  return last;
+  if (W.lane == 0) lds_st(&W.C.S->cons[W.c], end);
 }
 
-// marks `fin` finalised (all its reads of S->in and S->red are done) for the exchange wave;
-// called by the finalising wave after its last LDS read and before its exchange stores
-__device__ __forceinline__ void mark_done(Shared* S, u32 fin) {
-  lds_release();
-  if (__lane_id() == 0) lds_st(&S->done[fin & 1], fin + 1);
+// polls a quarter (128 slots = 256 values) of a 1024-value H2 vector into vin;
+// returns the lane's sum of squares of its 4 values
+__device__ __forceinline__ float poll_quarter1024(CW& W, u32 tag, long base_slot, float* vin) {
+  const int lane = W.lane;
+  const int voff[1] = {16 * lane};
+  v4u v[1];
+  poll<1>(W.C, tag, voff, (int)((base_slot + 128 * W.c) * 8), true, v);
+  const float a = lo_h(v[0].x), b = hi_h(v[0].x), cc = lo_h(v[0].z), d = hi_h(v[0].z);
+  *(float4*)(vin + 256 * W.c + 4 * lane) = make_float4(a, b, cc, d);
+  return a * a + b * b + cc * cc + d * d;
 }
 
-__device__ __forceinline__ void trace_mark(const KParams& P, int token, u32 fin_in_token, int what) {
-  if (P.trace && token == P.trace_token && __lane_id() == 0) {
-    const int FT = fins_per_token(P.mode, P.num_layers);
-    P.trace[((long)blockIdx.x * FT + fin_in_token) * TRACE_EVENTS + what] = wall_clock64();
-  }
+// loads a quarter of a 1024-value fp16 vector from global memory into vin (embedding row / MLP input)
+__device__ __forceinline__ float load_quarter1024(CW& W, const _Float16* src, float* vin) {
+  const h4 v = *(const h4*)(src + 256 * W.c + 4 * W.lane);
+  const float a = (float)v[0], b = (float)v[1], cc = (float)v[2], d = (float)v[3];
+  *(float4*)(vin + 256 * W.c + 4 * W.lane) = make_float4(a, b, cc, d);
+  return a * a + b * b + cc * cc + d * d;
 }
 
-__device__ __forceinline__ void compute(const KParams& P, Shared* S, const StageDesc& d, const Buf& b, CState& cs,
-                                        int w, int m, int c, int lane) {
-  const u32 fin = (u32)d.fin;
-  const float* in = S->in[fin & 1];
-  float* red = S->red[fin & 1];
-  const u32 epoch = P.epoch0 + (u32)d.token;
-  const int par = d.layer & 1;
-  const u32 fin_in_token = fin - (u32)(d.token * fins_per_token(P.mode, P.num_layers));
-  switch (d.type) {
-    case C_QKV: {
-      float part[4];
+__device__ __forceinline__ float rstd_of(const float* red) {
+  const float ss = (red[0] + red[1]) + (red[2] + red[3]);
+  return rsqrtf(ss * (1.0f / HIDDEN) + RMS_EPS);
+}
+
+// the lane's 16 normalised activations a = x[8 l .. 8 l + 8), b = x[512 + 8 l ..]
+__device__ __forceinline__ void norm_act(const float* vin, float rstd, const h8& w0, const h8& w1, float (&a)[8],
+                                         float (&b)[8], int lane) {
+  const float4 p0 = *(const float4*)(vin + 8 * lane), p1 = *(const float4*)(vin + 8 * lane + 4);
+  const float4 q0 = *(const float4*)(vin + 512 + 8 * lane), q1 = *(const float4*)(vin + 512 + 8 * lane + 4);
+  const float xa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+  const float xb[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part[r] = dot8(b.v[2 * r], in + 8 * lane) + dot8(b.v[2 * r + 1], in + 512 + 8 * lane);
-      // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
-      const float rs = reduce4(part[0], part[1], part[2], part[3]);
-      if ((lane & 15) == 0) red[4 * m + ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : (lane >> 4)))] = rs;
-      if (arrive(S, fin, NGW)) {
-        trace_mark(P, d.token, fin_in_token, TR_FSTART);
-        float v0 = 0.f, v1 = 0.f;
-        if (lane < QKV_PER_WG / 2) {
-          v0 = red[2 * lane];
-          v1 = red[2 * lane + 1];
-        }
-        mark_done(S, fin);
-        if (lane < QKV_PER_WG / 2)
-          ll_store(P.ws, slot_qkv(par, (QKV_PER_WG / 2) * w + lane), pack_h2(v0, v1), tag_of(epoch, d.layer, SID_QKV));
-        trace_mark(P, d.token, fin_in_token, TR_FINAL);
-      }
-      break;
+  for (int e = 0; e < 8; ++e) {
+    a[e] = xa[e] * rstd * (float)w0[e];
+    b[e] = xb[e] * rstd * (float)w1[e];
+  }
+}
+
+// one 2 KB weight row held in ring lines n, n + 1 dotted with (a | b)
+__device__ __forceinline__ float row2k(Shared* S, u32 n, int lane, const float (&a)[8], const float (&b)[8]) {
+  return dot8(ring_line(S, n)[lane], a) + dot8(ring_line(S, n + 1)[lane], b);
+}
+
+// ---- stages ----------------------------------------------------------------------------
+
+// QKV: rows [16 i + 4 c, +4) of the kv group from the normalised residual
+__device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u32 epoch, int token) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const LDGLayerWeight& lw = S->lw[l];
+  const h8 w0 = *(const h8*)((const _Float16*)lw.input_layernorm_weight + 8 * lane);
+  const h8 w1 = *(const h8*)((const _Float16*)lw.input_layernorm_weight + 512 + 8 * lane);
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_POLL);
+  float ss;
+  if (l == 0) {
+    const _Float16* row = P.embed + (long)token * HIDDEN;
+    ss = load_quarter1024(W, row, S->vin[p]);
+    if (W.c == 0 && lane < HROWS) S->resid[lane] = (float)row[HROWS * W.i + lane];
+  } else {
+    ss = poll_quarter1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), S->vin[p]);
+  }
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
+  ss = wave_sum(ss);
+  if (lane == 0) S->red[p][W.c] = ss;
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_SYNC);
+  float a[8], b[8];
+  norm_act(S->vin[p], rstd_of(S->red[p]), w0, w1, a, b, lane);
+  const u32 n0 = W.gl;
+  W.gl += LINES_QKV;
+  wait_lines(W, W.gl);
+  float part[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + 2 * (4 * W.c + r), lane, a, b);
+  release_lines(W, W.gl);
+  // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
+  const float rs = reduce4(part[0], part[1], part[2], part[3]);
+  const float r0 = bcast(rs, 0), r1 = bcast(rs, 32), r2 = bcast(rs, 16), r3 = bcast(rs, 48);
+  if (lane < 2)
+    ll_store(P.ws, xbuf(par, W.x, B_QKV) + (QKV_PER_WG / 2) * W.i + 2 * W.c + lane,
+             lane == 0 ? pack_h2(r0, r1) : pack_h2(r2, r3), tag_of(epoch, l, S_QKV));
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// attention split i of kv head x: q/k norms, RoPE, K/V write, 16 positions per wave, merge
+__device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u32 epoch) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const LDGLayerWeight& lw = S->lw[l];
+  const int pos = P.start_pos + t, ctx = pos + 1;
+  const int d4 = 4 * (lane & 31);
+  const h4 cv = *(const h4*)(P.cos_t + (long)pos * HD + d4);
+  const h4 sv = *(const h4*)(P.sin_t + (long)pos * HD + d4);
+  const h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d4);
+  const h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d4);
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_POLL);
+  {  // quarter c: slots [64 c, 64 c + 64) of the group's 256 q|k|v slots
+    const int voff[1] = {16 * lane};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, S_QKV), voff, (int)((xbuf(par, W.x, B_QKV) + 64 * W.c) * 8), lane < 32, v);
+    if (lane < 32)
+      *(float4*)(S->vin[p] + 128 * W.c + 4 * lane) =
+          make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
+  }
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_SYNC);
+  // every wave computes the same normed, roped q0 | q1 | k and v (identical writes to qr)
+  {
+    const float4 qv = *(const float4*)(S->vin[p] + 4 * lane);        // q head (lane / 32), dims d4
+    const float4 kv = *(const float4*)(S->vin[p] + 256 + 4 * lane);  // k (lane < 32) or v, dims d4
+    const float q[4] = {qv.x, qv.y, qv.z, qv.w};
+    const float k[4] = {kv.x, kv.y, kv.z, kv.w};
+    const float rq = rsqrtf(half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]) * (1.0f / HD) + RMS_EPS);
+    const float rk = rsqrtf(half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]) * (1.0f / HD) + RMS_EPS);
+    float qq[4], kk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      qq[j] = q[j] * rq * (float)qn[j];
+      kk[j] = k[j] * rk * (float)kn[j];
     }
-    case C_ATT: {
-      const int pos = P.start_pos + d.token, ctx = pos + 1;
-      const int g = att_kv(w), s = att_split(w);
-      const int t0 = att_t0(ctx, s), t1 = att_t1(ctx, s);
-      const int j = lane >> 4, q = lane & 15;
-      const float* q0 = in;
-      const float* q1 = in + 128;
-      const float* kr = in + 256;
-      const float* vr = in + 384;
-      float4 qa0 = *(const float4*)(q0 + 8 * q), qb0 = *(const float4*)(q0 + 8 * q + 4);
-      float4 qa1 = *(const float4*)(q1 + 8 * q), qb1 = *(const float4*)(q1 + 8 * q + 4);
-      const float qv0[8] = {qa0.x, qa0.y, qa0.z, qa0.w, qb0.x, qb0.y, qb0.z, qb0.w};
-      const float qv1[8] = {qa1.x, qa1.y, qa1.z, qa1.w, qb1.x, qb1.y, qb1.z, qb1.w};
-      float sc[4][2];
-      bool valid[4];
+    // rotate-half RoPE: partner dims d +- 64 live in lane ^ 16
+    const bool lo_half = (lane & 31) < 16;
+    float qo[4], ko[4];
 #pragma unroll
-      for (int bb = 0; bb < 4; ++bb) {
-        const int p = t0 + att_local_pos(m, j, bb);
-        valid[bb] = p < t1;
-        float kf[8];
-        if (p == pos) {
+    for (int j = 0; j < 4; ++j) {
+      const float qp = xor16(qq[j]), kp = xor16(kk[j]);
+      const float cs = (float)cv[j], sn = lo_half ? -(float)sv[j] : (float)sv[j];
+      qo[j] = qq[j] * cs + qp * sn;
+      ko[j] = kk[j] * cs + kp * sn;
+    }
+    *(float4*)(S->qr + 4 * lane) = make_float4(qo[0], qo[1], qo[2], qo[3]);
+    if (lane < 32)
+      *(float4*)(S->qr + 256 + 4 * lane) = make_float4(ko[0], ko[1], ko[2], ko[3]);
+    else
+      *(float4*)(S->qr + 256 + 4 * lane) = make_float4(k[0], k[1], k[2], k[3]);
+    // the split holding `pos` writes this position's K (roped) and V to the cache
+    if (W.c == 0 && att_t0(ctx, W.i) <= pos && pos < att_t1(ctx, W.i)) {
+      const long row = (((long)l * NKV + W.x) * P.max_seq + pos) * HD + d4;
+      if (lane < 32) {
+        const h4 o = {(_Float16)ko[0], (_Float16)ko[1], (_Float16)ko[2], (_Float16)ko[3]};
+        *(h4*)(P.k_cache + row) = o;
+      } else {
+        const h4 o = {(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
+        *(h4*)(P.v_cache + row) = o;
+      }
+    }
+  }
+  // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..
+  const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
+  const u32 n0 = W.gl;
+  W.gl += 2 * nk;
+  const int j = lane >> 4, q16 = lane & 15;
+  float qa[8], qb[8], kc[8], vc[8];
+  {
+    const float4 a0 = *(const float4*)(S->qr + 8 * q16), a1 = *(const float4*)(S->qr + 8 * q16 + 4);
+    const float4 b0 = *(const float4*)(S->qr + 128 + 8 * q16), b1 = *(const float4*)(S->qr + 128 + 8 * q16 + 4);
+    const float4 k0 = *(const float4*)(S->qr + 256 + 8 * q16), k1 = *(const float4*)(S->qr + 256 + 8 * q16 + 4);
+    const float4 v0 = *(const float4*)(S->qr + 384 + 8 * q16), v1 = *(const float4*)(S->qr + 384 + 8 * q16 + 4);
+    const float aa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kf[e] = (float)(_Float16)kr[8 * q + e];  // the cached value is fp16
+    for (int e = 0; e < 8; ++e) {
+      qa[e] = aa[e];
+      qb[e] = bb[e];
+      kc[e] = (float)(_Float16)kk[e];  // the current position's k and v as the cache holds them
+      vc[e] = (float)(_Float16)vv[e];
+    }
+  }
+  wait_lines(W, W.gl);
+  float sc[4][2];
+  bool valid[4], cur[4];
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const int m = 4 * W.c + bb;
+    const int pp = t0 + 4 * m + j;
+    valid[bb] = m < nk && pp < t1;
+    cur[bb] = pp == pos;
+    float s0 = 0.f, s1 = 0.f;
+    if (m < nk) {
+      float kf[8];
+      if (cur[bb]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] = kc[e];
+      } else {
+        const h8 kh = __builtin_bit_cast(h8, ring_line(S, n0 + m)[lane]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] = (float)kh[e];
+      }
+      s0 = kf[0] * qa[0];
+      s1 = kf[0] * qb[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) {
+        s0 = fmaf(kf[e], qa[e], s0);
+        s1 = fmaf(kf[e], qb[e], s1);
+      }
+    }
+    s0 = row16_sum(s0) * P.attn_scale;
+    s1 = row16_sum(s1) * P.attn_scale;
+    sc[bb][0] = valid[bb] ? s0 : -INFINITY;
+    sc[bb][1] = valid[bb] ? s1 : -INFINITY;
+  }
+  float mh[2], lh[2], acc[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float mx = rows4_max(fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h])));
+    mh[h] = mx;
+    float pr[4], lsum = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      pr[bb] = valid[bb] ? __expf(sc[bb][h] - mx) : 0.f;
+      lsum += pr[bb];
+    }
+    lh[h] = rows4_sum(lsum);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+      const int m = 4 * W.c + bb;
+      if (m < nk) {
+        float vf[8];
+        if (cur[bb]) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = vc[e];
         } else {
-          h8 kh = __builtin_bit_cast(h8, b.v[bb]);
+          const h8 vh = __builtin_bit_cast(h8, ring_line(S, n0 + nk + m)[lane]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) kf[e] = (float)kh[e];
+          for (int e = 0; e < 8; ++e) vf[e] = (float)vh[e];
         }
-        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          s0 = fmaf(kf[e], qv0[e], s0);
-          s1 = fmaf(kf[e], qv1[e], s1);
-        }
-        s0 = row16_sum(s0) * P.attn_scale;
-        s1 = row16_sum(s1) * P.attn_scale;
-        sc[bb][0] = valid[bb] ? s0 : -INFINITY;
-        sc[bb][1] = valid[bb] ? s1 : -INFINITY;
+        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pr[bb], vf[e], acc[h][e]);
       }
-      float mh[2], lh[2], acc[2][8];
+    }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float mx = fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h]));
-        mx = rows4_max(mx);
-        mh[h] = mx;
-        float pr[4];
-        float l = 0.f;
+    for (int e = 0; e < 8; ++e) acc[h][e] = rows4_sum(acc[h][e]);
+  }
+  release_lines(W, W.gl);
+  float* rec = &S->apart[W.c][0][0];
+  if (lane < 16) {
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-          pr[bb] = valid[bb] ? __expf(sc[bb][h] - mx) : 0.f;
-          l += pr[bb];
-        }
-        l = rows4_sum(l);
-        lh[h] = l;
+    for (int h = 0; h < 2; ++h) {
+      *(float4*)(rec + h * PART_PER_HEAD + 2 + 8 * q16) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      *(float4*)(rec + h * PART_PER_HEAD + 2 + 8 * q16 + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    }
+  }
+  if (lane == 0) {
+    rec[0] = mh[0];
+    rec[1] = lh[0];
+    rec[PART_PER_HEAD] = mh[1];
+    rec[PART_PER_HEAD + 1] = lh[1];
+  }
+  sync4(W);
+  // merge the 4 wave partials: wave c writes entries [65 c, 65 c + 65) of the 260
+  float Mx[2], wt[2][NCW];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  for (int h = 0; h < 2; ++h) {
+    float M = -INFINITY;
 #pragma unroll
-        for (int bb = 0; bb < 4; ++bb) {
-          const int p = t0 + att_local_pos(m, j, bb);
-          float vf[8];
-          if (p == pos) {
+    for (int cc = 0; cc < NCW; ++cc) M = fmaxf(M, S->apart[cc][h][0]);
+    Mx[h] = M;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = (float)(_Float16)vr[8 * q + e];
-          } else {
-            h8 vh = __builtin_bit_cast(h8, b.v[4 + bb]);
+    for (int cc = 0; cc < NCW; ++cc) {
+      const float mc = S->apart[cc][h][0];
+      wt[h][cc] = (mc == -INFINITY) ? 0.f : __expf(mc - M);
+    }
+  }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = (float)vh[e];
-          }
+  for (int it = 0; it < 2; ++it) {
+    if (it == 0 || lane == 0) {
+      const int e = 65 * W.c + (it == 0 ? lane : 64);
+      const int h = e >= PART_PER_HEAD ? 1 : 0;
+      const int k = e - PART_PER_HEAD * h;
+      float val = 0.f;
+      if (k == 0) {
+        val = Mx[h];
+      } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pr[bb], vf[e], acc[h][e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          acc[h][e] = rows4_sum(acc[h][e]);
-        }
+        for (int cc = 0; cc < NCW; ++cc) val = fmaf(h ? wt[1][cc] : wt[0][cc], S->apart[cc][h][k], val);
       }
-      float* rec = red + m * 260;
-      if (lane < 16) {
+      ll_store(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
+    }
+  }
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// combine (wave 0): q head 2x + i / 16, dims [8 (i % 16), +8) over the 32 splits
+__device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u32 epoch) {
+  if (W.c != 0) return;
+  const int lane = W.lane, par = l & 1;
+  const int hh = W.i / 16, d0 = 8 * (W.i % 16);
+  const int s = lane & 31;
+  int voff[5];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          *(float4*)(rec + h * 130 + 2 + 8 * q) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-          *(float4*)(rec + h * 130 + 2 + 8 * q + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-        }
+  for (int k = 0; k < 5; ++k) voff[k] = (int)(part_index(s, hh, k == 0 ? 0 : 2 + d0 + 2 * (k - 1)) * 8);
+  v4u v[5];
+  trace_ev(P, t, NSTAGE * l + S_COMB, TR_POLL);
+  poll<5>(W.C, tag_of(epoch, l, S_ATT), voff, (int)(xbuf(par, W.x, B_PART) * 8), lane < NSPLIT, v);
+  trace_ev(P, t, NSTAGE * l + S_COMB, TR_INPUT);
+  float m = -INFINITY, lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (lane < NSPLIT) {
+    m = __uint_as_float(v[0].x);
+    lsum = __uint_as_float(v[0].z);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc[2 * k] = __uint_as_float(v[k + 1].x);
+      acc[2 * k + 1] = __uint_as_float(v[k + 1].z);
+    }
+  }
+  const float M = max16x(row16_max(m));  // over lanes 0-31 (lanes >= 32 hold -inf)
+  const float e = (lane < NSPLIT && m != -INFINITY) ? __expf(m - M) : 0.f;
+  const float Lt = half_sum(e * lsum);
+  float o[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = half_sum(e * acc[k]);
+  const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+  // lane k < 4 stores dims 2k, 2k+1 (static selects: no lane-indexed array)
+  const float oa = lane == 0 ? o[0] : (lane == 1 ? o[2] : (lane == 2 ? o[4] : o[6]));
+  const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
+  if (lane < 4)
+    ll_store(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + lane, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
+  trace_ev(P, t, NSTAGE * l + S_COMB, TR_STORE);
+}
+
+// o_proj partial of the XCD: rows [32 i + 8 c, +8) over the XCD's 256 attention dims
+__device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 epoch) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  trace_ev(P, t, NSTAGE * l + S_O, TR_POLL);
+  {  // quarter c: slots [32 c, 32 c + 32) = values [64 c, 64 c + 64)
+    const int voff[1] = {16 * lane};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, S_COMB), voff, (int)((xbuf(par, W.x, B_ATTO) + 32 * W.c) * 8), lane < 16, v);
+    if (lane < 16)
+      *(float4*)(S->vin[p] + 64 * W.c + 4 * lane) =
+          make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
+  }
+  trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_O, TR_SYNC);
+  float a[8];
+  {
+    const float4 a0 = *(const float4*)(S->vin[p] + 8 * (lane & 31)), a1 = *(const float4*)(S->vin[p] + 8 * (lane & 31) + 4);
+    a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
+  }
+  const u32 n0 = W.gl;
+  W.gl += LINES_O;
+  wait_lines(W, W.gl);
+  // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
+  float part[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) part[m] = dot8(ring_line(S, n0 + 4 * W.c + m)[lane], a);
+  release_lines(W, W.gl);
+  // y0 rows: (line 0 lo, line 1 lo, line 0 hi, line 1 hi) = rows 8c + (0, 2, 1, 3); y1 = +4
+  const float y0 = row16_sum(pack16(part[0], part[1])), y1 = row16_sum(pack16(part[2], part[3]));
+  if ((lane & 15) == 0) {
+    const int r = 8 * W.c + reduce8_row(lane);
+    const long base = xbuf(par, W.x, B_OP) + HROWS * W.i;
+    ll_store(P.ws, base + r, __float_as_uint(y0), tag_of(epoch, l, S_O));
+    ll_store(P.ws, base + r + 4, __float_as_uint(y1), tag_of(epoch, l, S_O));
+  }
+  trace_ev(P, t, NSTAGE * l + S_O, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// sum of the 8 per-XCD partials of rows [32 i, 32 i + 32) plus the residual;
+// `src` is B_OP (o_proj, producing the post-attention residual) or B_DP (down,
+// producing the next layer's residual)
+__device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u32 epoch, bool is_down) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int st = is_down ? S_DSUM : S_OSUM;
+  trace_ev(P, t, NSTAGE * l + st, TR_POLL);
+  {  // XCDs 2c, 2c + 1: lane < 32 reads XCD 2c + lane / 16, rows 2 (lane % 16), +1
+    const int g = 2 * W.c + ((lane >> 4) & 1);
+    const long src0 = xbuf(par, 2 * W.c, is_down ? B_DP : B_OP) + HROWS * W.i;
+    const int voff[1] = {(int)(((long)((lane >> 4) & 1) * XCD_SLOTS + 2 * (lane & 15)) * 8)};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, is_down ? S_DOWN : S_O), voff, (int)(src0 * 8), lane < 32, v);
+    if (lane < 32) {
+      S->opart[p][g][2 * (lane & 15)] = __uint_as_float(v[0].x);
+      S->opart[p][g][2 * (lane & 15) + 1] = __uint_as_float(v[0].z);
+    }
+  }
+  trace_ev(P, t, NSTAGE * l + st, TR_INPUT);
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + st, TR_SYNC);
+  if (lane < 4) {  // rows 8c + 2 lane, +1
+    const int r = 8 * W.c + 2 * lane;
+    float s0 = is_down ? S->actres[r] : S->resid[r];
+    float s1 = is_down ? S->actres[r + 1] : S->resid[r + 1];
+#pragma unroll
+    for (int g = 0; g < NXCD; ++g) {
+      s0 += S->opart[p][g][r];
+      s1 += S->opart[p][g][r + 1];
+    }
+    if (is_down) {
+      S->resid[r] = s0;
+      S->resid[r + 1] = s1;
+    } else {
+      S->actres[r] = s0;
+      S->actres[r + 1] = s1;
+    }
+    if (P.mode == MODE_MLP) {
+      if (W.x == 0) {
+        P.out_vec[HROWS * W.i + r] = s0;
+        P.out_vec[HROWS * W.i + r + 1] = s1;
       }
-      if (lane == 0) {
-        rec[0] = mh[0];
-        rec[1] = lh[0];
-        rec[130] = mh[1];
-        rec[131] = lh[1];
+    } else {
+      ll_store(P.ws, xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 4 * W.c + lane, pack_h2(s0, s1),
+               tag_of(epoch, l, st));
+      if (is_down && l == P.num_layers - 1 && W.x == 0) {  // final-layer residual
+        const int row = HROWS * W.i + r;
+        if (P.hidden_steps) {
+          P.hidden_steps[(long)t * HIDDEN + row] = s0;
+          P.hidden_steps[(long)t * HIDDEN + row + 1] = s1;
+        }
+        P.hidden_out[row] = (_Float16)s0;
+        P.hidden_out[row + 1] = (_Float16)s1;
       }
-      if (arrive(S, fin, NGW)) {
-        trace_mark(P, d.token, fin_in_token, TR_FSTART);
-        // merge the 4 wave partials into the workgroup partial (m, l, acc) per head
-        float Mx[2], wt[2][NGW];
+    }
+  }
+  trace_ev(P, t, NSTAGE * l + st, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// gate/up rows 384 x + 12 i + 3 c + {0, 1, 2} -> SiLU(gate) * up
+__device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32 epoch) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const LDGLayerWeight& lw = S->lw[l];
+  const h8 w0 = *(const h8*)((const _Float16*)lw.post_attn_layernorm_weight + 8 * lane);
+  const h8 w1 = *(const h8*)((const _Float16*)lw.post_attn_layernorm_weight + 512 + 8 * lane);
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_POLL);
+  float ss;
+  if (P.mode == MODE_MLP) {
+    ss = load_quarter1024(W, P.in_vec, S->vin[p]);
+    if (W.c == 0 && lane < HROWS) S->actres[lane] = (float)P.in_vec[HROWS * W.i + lane];
+  } else {
+    ss = poll_quarter1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), S->vin[p]);
+  }
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
+  ss = wave_sum(ss);
+  if (lane == 0) S->red[p][W.c] = ss;
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_SYNC);
+  float a[8], b[8];
+  norm_act(S->vin[p], rstd_of(S->red[p]), w0, w1, a, b, lane);
+  const u32 n0 = W.gl;
+  W.gl += LINES_GU;
+  wait_lines(W, W.gl);
+  float part[6];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float M = -INFINITY;
+  for (int jj = 0; jj < 3; ++jj) {
+    part[jj] = row2k(S, n0 + 2 * (3 * W.c + jj), lane, a, b);                          // gate
+    part[3 + jj] = row2k(S, n0 + 2 * GU_PER_WG + 2 * (3 * W.c + jj), lane, a, b);      // up
+  }
+  release_lines(W, W.gl);
+  float pq, qq;
+  reduce6(part, pq, qq);  // pq rows: gate0, gate1, up0, up1; qq rows: gate2, gate2, up2, up2
+  const float g0 = bcast(pq, 0), g1 = bcast(pq, 16), u0 = bcast(pq, 32), u1 = bcast(pq, 48);
+  const float g2 = bcast(qq, 0), u2 = bcast(qq, 32);
+  const float s0 = g0 / (1.0f + __expf(-g0)) * u0;
+  const float s1 = g1 / (1.0f + __expf(-g1)) * u1;
+  const float s2 = g2 / (1.0f + __expf(-g2)) * u2;
+  if (lane < 2)
+    ll_store(P.ws, xbuf(par, W.x, B_INT) + int_slot(W.i, W.c, lane), lane == 0 ? pack_h2(s0, s1) : pack_h2(s2, 0.f),
+             tag_of(epoch, l, S_GU));
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// down partial of the XCD: rows [32 i + 8 c, +8) over the XCD's 384 inter values
+__device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u32 epoch) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, par = l & 1, p = W.par_in;
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_POLL);
+  {  // quarter c: slots [64 c, 64 c + 64): pair k = 32 c + lane = workgroup k / 4, wave k % 4
+    const int voff[1] = {16 * lane};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, S_GU), voff, (int)((xbuf(par, W.x, B_INT) + 64 * W.c) * 8), lane < 32, v);
+    if (lane < 32) {
+      const int k = 32 * W.c + lane;
+      float* dst = S->vin[p] + GU_PER_WG * (k >> 2) + 3 * (k & 3);
+      dst[0] = lo_h(v[0].x);
+      dst[1] = hi_h(v[0].x);
+      dst[2] = lo_h(v[0].z);
+    }
+  }
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
+  sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_SYNC);
+  float a[8];
+  {  // lanes 0-47 own inter values [8 l, 8 l + 8); lanes 48-63 contribute nothing
+    const int o = lane < 48 ? 8 * lane : 0;
+    const float4 a0 = *(const float4*)(S->vin[p] + o), a1 = *(const float4*)(S->vin[p] + o + 4);
+    const float z = lane < 48 ? 1.f : 0.f;
+    a[0] = a0.x * z; a[1] = a0.y * z; a[2] = a0.z * z; a[3] = a0.w * z;
+    a[4] = a1.x * z; a[5] = a1.y * z; a[6] = a1.z * z; a[7] = a1.w * z;
+  }
+  const u32 n0 = W.gl;
+  W.gl += LINES_DOWN;
+  wait_lines(W, W.gl);
+  float part[8];
 #pragma unroll
-          for (int cc = 0; cc < NGW; ++cc) M = fmaxf(M, red[cc * 260 + h * 130]);
-          Mx[h] = M;
-#pragma unroll
-          for (int cc = 0; cc < NGW; ++cc) {
-            const float mc = red[cc * 260 + h * 130];
-            wt[h][cc] = (mc == -INFINITY) ? 0.f : __expf(mc - M);
-          }
-        }
-        float vals[5];
-#pragma unroll
-        for (int it = 0; it < 5; ++it) {
-          const int e = lane + 64 * it;
-          vals[it] = 0.f;
-          if (e < 260) {
-            const bool h1 = e >= 130;
-            const int k = h1 ? e - 130 : e;
-            if (k == 0) {
-              vals[it] = h1 ? Mx[1] : Mx[0];
-            } else {
-#pragma unroll
-              for (int cc = 0; cc < NGW; ++cc)
-                vals[it] = fmaf(h1 ? wt[1][cc] : wt[0][cc], red[cc * 260 + e], vals[it]);
-            }
-          }
-        }
-        mark_done(S, fin);
-#pragma unroll
-        for (int it = 0; it < 5; ++it) {
-          const int e = lane + 64 * it;
-          if (e < 260) {
-            const bool h1 = e >= 130;
-            ll_store(P.ws, slot_part(par, g, s, h1 ? 1 : 0, h1 ? e - 130 : e), __float_as_uint(vals[it]),
-                     tag_of(epoch, d.layer, SID_PART));
-          }
-        }
-        trace_mark(P, d.token, fin_in_token, TR_FINAL);
-      }
+  for (int r = 0; r < 8; ++r) part[r] = dot8(ring_line(S, n0 + 8 * W.c + r)[lane], a);
+  release_lines(W, W.gl);
+  float y0, y1;
+  reduce8(part, y0, y1);
+  if ((lane & 15) == 0) {
+    const int r = 8 * W.c + reduce8_row(lane);
+    const long base = xbuf(par, W.x, B_DP) + HROWS * W.i;
+    ll_store(P.ws, base + r, __float_as_uint(y0), tag_of(epoch, l, S_DOWN));
+    ll_store(P.ws, base + r + 4, __float_as_uint(y1), tag_of(epoch, l, S_DOWN));
+  }
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_STORE);
+  W.par_in ^= 1;
+}
+
+// lm_head input: final RMSNorm of the all-gathered residual (decode) or the caller's vector
+__device__ __forceinline__ void st_lm_input(CW& W, const KParams& P, int t, u32 epoch) {
+  Shared* S = W.C.S;
+  const int lane = W.lane, p = W.par_in, L = P.num_layers;
+  const int o = 256 * W.c + 4 * lane;
+  if (P.mode == MODE_LMHEAD) {
+    const h4 v = *(const h4*)(P.in_vec + o);
+    *(float4*)(S->xfin + o) = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+  } else {
+    const h4 wf = *(const h4*)(P.final_norm + o);
+    trace_ev(P, t, NSTAGE * L, TR_POLL);
+    float ss = poll_quarter1024(W, tag_of(epoch, L - 1, S_DSUM), xbuf((L - 1) & 1, W.x, B_X), S->vin[p]);
+    trace_ev(P, t, NSTAGE * L, TR_INPUT);
+    ss = wave_sum(ss);
+    if (lane == 0) S->red[p][W.c] = ss;
+    sync4(W);
+    trace_ev(P, t, NSTAGE * L, TR_SYNC);
+    const float rs = rstd_of(S->red[p]);
+    const float4 xv = *(const float4*)(S->vin[p] + o);
+    const float4 nv = make_float4(xv.x * rs * (float)wf[0], xv.y * rs * (float)wf[1], xv.z * rs * (float)wf[2],
+                                  xv.w * rs * (float)wf[3]);
+    *(float4*)(S->xfin + o) = nv;
+    if (W.w == 0) *(float4*)(P.norm_out + o) = nv;
+    W.par_in ^= 1;
+  }
+  lds_release();
+  if (lane == 0) __hip_atomic_fetch_add(&S->xfin_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c) {
+  CW W;
+  W.C.P = &P;
+  W.C.S = S;
+  W.C.r = ws_rsrc(P.ws);
+  W.C.ok = true;
+  W.C.deadline = P.deadline;
+  W.w = blockIdx.x;
+  W.x = xcd_of(W.w);
+  W.i = loc_of(W.w);
+  W.c = c;
+  W.lane = __lane_id();
+  W.nsync = 0;
+  W.par_in = 0;
+  W.gl = 0;
+  const int L = P.num_layers;
+  int token = P.first_token;
+  u32 phase = 0;
+  for (int t = 0; t < P.num_steps && W.C.ok; ++t) {
+    const u32 epoch = P.epoch0 + (u32)t;
+    if (P.mode == MODE_MLP) {
+      st_gu(W, P, t, 0, epoch);
+      st_down(W, P, t, 0, epoch);
+      st_sum(W, P, t, 0, epoch, true);
       break;
     }
-    case C_OPROJ: {
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) sum += dot8(b.v[k], in + 8 * lane + 512 * k);
-      sum = wave_sum(sum);
-      if (lane == 0) red[m] = sum;
-      if (arrive(S, fin, NGW)) {
-        trace_mark(P, d.token, fin_in_token, TR_FSTART);
-        float a0 = 0.f, a1 = 0.f;
-        if (lane < 2) {
-          const int r0 = 2 * lane;
-          a0 = red[r0] + S->xres[r0];
-          a1 = red[r0 + 1] + S->xres[r0 + 1];
-          S->actres[r0] = a0;
-          S->actres[r0 + 1] = a1;
-        }
-        mark_done(S, fin);
-        if (lane < 2) ll_store(P.ws, slot_act(par, 2 * w + lane), pack_h2(a0, a1), tag_of(epoch, d.layer, SID_ACT));
-        trace_mark(P, d.token, fin_in_token, TR_FINAL);
+    if (P.mode == MODE_DECODE) {
+      for (int l = 0; l < L && W.C.ok; ++l) {
+        st_qkv(W, P, t, l, epoch, token);
+        st_att(W, P, t, l, epoch);
+        st_comb(W, P, t, l, epoch);
+        st_o(W, P, t, l, epoch);
+        st_sum(W, P, t, l, epoch, false);
+        st_gu(W, P, t, l, epoch);
+        st_down(W, P, t, l, epoch);
+        st_sum(W, P, t, l, epoch, true);
       }
-      break;
+      if (!W.C.ok) break;
     }
-    case C_GU: {
-      float part[6];
+    st_lm_input(W, P, t, epoch);
+    ++phase;
+    lm_rows(W.C, P, c, t, phase);
+    // workgroup partial -> ARG slots; every workgroup then reduces all 256
+    if (c == 0) {
+      lds_wait_ge(W.C, &S->lm_cnt, (NCW + NLW) * phase);
+      float best = -INFINITY;
+      int bidx = 0x7fffffff;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) part[k] = dot8(b.v[2 * k], in + 8 * lane) + dot8(b.v[2 * k + 1], in + 512 + 8 * lane);
-      float pr, qr;
-      reduce6(part, pr, qr);  // pr: rows 0,1,3,4 at lanes 0,16,32,48; qr: rows 2 (lane 0), 5 (lane 32)
-      if ((lane & 15) == 0) red[6 * m + (lane >> 4) + ((lane >> 4) >= 2 ? 1 : 0)] = pr;
-      if ((lane & 31) == 0) red[6 * m + (lane == 0 ? 2 : 5)] = qr;
-      if (arrive(S, fin, NGW)) {
-        trace_mark(P, d.token, fin_in_token, TR_FSTART);
-        float o[2] = {0.f, 0.f};
-        if (lane < INT_PER_WG / 2) {
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const float gt = red[2 * lane + e], up = red[INT_PER_WG + 2 * lane + e];
-            o[e] = gt / (1.0f + __expf(-gt)) * up;
-          }
-        }
-        mark_done(S, fin);
-        if (lane < INT_PER_WG / 2)
-          ll_store(P.ws, slot_int(par, (INT_PER_WG / 2) * w + lane), pack_h2(o[0], o[1]), tag_of(epoch, d.layer, SID_INT));
-        trace_mark(P, d.token, fin_in_token, TR_FINAL);
+      for (int v = 0; v < NCW + NLW; ++v) better(best, bidx, S->lmv[v], S->lmi[v]);
+      if (W.lane == 0) {
+        const u32 tg = tag_arg(epoch);
+        ll_store(P.ws, slot_arg(t & 1, 2 * W.w), __float_as_uint(best), tg);
+        ll_store(P.ws, slot_arg(t & 1, 2 * W.w + 1), (u32)bidx, tg);
       }
-      break;
     }
-    case C_DOWN: {
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < 6; ++k) sum += dot8(b.v[k], in + 8 * lane + 512 * k);
-      sum = wave_sum(sum);
-      if (lane == 0) red[m] = sum;
-      if (arrive(S, fin, NGW)) {
-        trace_mark(P, d.token, fin_in_token, TR_FSTART);
-        float x0 = 0.f, x1 = 0.f;
-        if (lane < 2) {
-          const int r0 = 2 * lane;
-          x0 = red[r0] + S->actres[r0];
-          x1 = red[r0 + 1] + S->actres[r0 + 1];
-          S->xres[r0] = x0;
-          S->xres[r0 + 1] = x1;
-        }
-        mark_done(S, fin);
-        if (lane < 2) {
-          if (P.mode == MODE_MLP) {
-            P.out_vec[HID_PER_WG * w + 2 * lane] = x0;
-            P.out_vec[HID_PER_WG * w + 2 * lane + 1] = x1;
-          } else {
-            ll_store(P.ws, slot_x((d.layer + 1) & 1, 2 * w + lane), pack_h2(x0, x1), tag_of(epoch, d.layer, SID_X));
-          }
-        }
-        trace_mark(P, d.token, fin_in_token, TR_FINAL);
+    {
+      const int voff[1] = {16 * W.lane};
+      v4u v[1];
+      poll<1>(W.C, tag_arg(epoch), voff, (int)(slot_arg(t & 1, 128 * c) * 8), true, v);
+      float best = __uint_as_float(v[0].x);
+      int bidx = (int)v[0].z;
+      wave_argmax(best, bidx);
+      if (W.lane == 0) {
+        S->argv[c] = best;
+        S->argi[c] = bidx;
       }
-      break;
+      sync4(W);
+      best = -INFINITY;
+      bidx = 0x7fffffff;
+#pragma unroll
+      for (int cc = 0; cc < NCW; ++cc) better(best, bidx, S->argv[cc], S->argi[cc]);
+      if (bidx < 0 || bidx >= VOCAB) bidx = 0;  // every logit NaN
+      if (W.w == 0 && c == 0 && W.lane == 0) P.out_tokens[t] = bidx;
+      trace_ev(P, t, NSTAGE * L, TR_STORE);
+      token = (P.forced && t + 1 < P.num_steps) ? P.forced[t + 1] : bidx;
+      if (token < 0 || token >= VOCAB) {  // a forced id out of range: report and stop
+        __hip_atomic_fetch_or(P.status, ST_BAD_TOKEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        W.C.ok = false;
+      }
     }
-    default: {  // C_LMH chunk: this wave's 6 rows of chunk d.chunk
-      if (d.chunk < 2) {  // first chunk this wave sees in this token
-        cs.lm_best = -INFINITY;
-        cs.lm_idx = 0x7fffffff;
-      }
-      const int nrows = lm_rows(w), r0 = lm_row0(w);
-      float part[LM_ROWS_PER_CHUNK];
-#pragma unroll
-      for (int i = 0; i < LM_ROWS_PER_CHUNK; ++i)
-        part[i] = dot8(b.v[2 * i], in + 8 * lane) + dot8(b.v[2 * i + 1], in + 512 + 8 * lane);
-      float pr, qr;
-      reduce6(part, pr, qr);
-      // lane 0: rows 0 (pr), 2 (qr); lane 16: row 1; lane 32: rows 3 (pr), 5 (qr); lane 48: row 4.
-      // Each lane's rows ascend across chunks, so strict > keeps the lowest index.
-      if ((lane & 15) == 0) {
-        const int ip = (lane >> 4) + ((lane >> 4) >= 2 ? 1 : 0);
-        const int lr = lm_local_row(m, d.chunk, ip);
-        if (lr < nrows) {
-          if (P.logits_out) P.logits_out[(long)d.token * VOCAB + r0 + lr] = pr;
-          const float v = __builtin_isnan(pr) ? -INFINITY : pr;
-          if (v > cs.lm_best) {
-            cs.lm_best = v;
-            cs.lm_idx = r0 + lr;
-          }
-        }
-      }
-      if ((lane & 31) == 0) {
-        const int lr = lm_local_row(m, d.chunk, lane == 0 ? 2 : 5);
-        if (lr < nrows) {
-          if (P.logits_out) P.logits_out[(long)d.token * VOCAB + r0 + lr] = qr;
-          const float v = __builtin_isnan(qr) ? -INFINITY : qr;
-          if (v > cs.lm_best) {
-            cs.lm_best = v;
-            cs.lm_idx = r0 + lr;
-          }
-        }
-      }
-      if (d.chunk >= LM_CHUNKS - 2) {  // this wave's last chunk of the token
-        float bv = cs.lm_best;
-        int bi = cs.lm_idx;
-        wave_argmax(bv, bi);
-        if (lane == 0) {
-          red[2 * c] = bv;
-          red[2 * c + 1] = __int_as_float(bi);
-        }
-        if (arrive(S, fin, NCW)) {
-          trace_mark(P, d.token, fin_in_token, TR_FSTART);
-          float best = -INFINITY;
-          int bidx = 0x7fffffff;
-          for (int cc = 0; cc < NCW; ++cc) {
-            const float v = red[2 * cc];
-            const int ix = __float_as_int(red[2 * cc + 1]);
-            if (v > best || (v == best && ix < bidx)) {
-              best = v;
-              bidx = ix;
-            }
-          }
-          mark_done(S, fin);
-          if (lane == 0) {
-            const u32 tg = tag_arg(epoch);
-            ll_store(P.ws, slot_arg(d.token & 1, 2 * w), __float_as_uint(best), tg);
-            ll_store(P.ws, slot_arg(d.token & 1, 2 * w + 1), (u32)bidx, tg);
-          }
-          trace_mark(P, d.token, fin_in_token, TR_FINAL);
-        }
-      }
-      break;
+  }
+  if (!W.C.ok) lds_st(&S->abort, 1u);
+}
+
+// ------------------------------------------------------------------------------------
+// loader waves: every ring line of every stage in execution order; wave q
+// handles the lines n == q (mod 4). The address of lane `lane`'s 16 bytes of
+// line m of a stage:
+
+__device__ __forceinline__ const void* line_src(const KParams& P, const Shared* S, int st, int l, int m, int x, int i,
+                                                int pos, int ctx, int lane) {
+  const LDGLayerWeight& lw = S->lw[l];
+  switch (st) {
+    case S_QKV: {
+      const int gr = QKV_PER_WG * i + (m >> 1);
+      const int mat = grp_matrix(gr);
+      const _Float16* W = (const _Float16*)(mat == 0 ? lw.q_proj_weight : (mat == 1 ? lw.k_proj_weight : lw.v_proj_weight));
+      return W + (long)grp_row_in(x, gr) * HIDDEN + 512 * (m & 1) + 8 * lane;
+    }
+    case S_ATT: {
+      const int nk = att_nk(ctx, i), t0 = att_t0(ctx, i), t1 = att_t1(ctx, i);
+      const bool is_v = m >= nk;
+      const int mm = is_v ? m - nk : m;
+      const int pp = t0 + 4 * mm + (lane >> 4);
+      const int lim = t1 < pos ? t1 : pos;  // positions already in the cache
+      // lanes without a cached position read the embedding's first row instead, so the
+      // DMA always covers all 64 lanes and no line of an unwritten position is cached
+      if (pp >= lim) return P.embed + 8 * lane;
+      const _Float16* base = is_v ? P.v_cache : P.k_cache;
+      return base + (((long)l * NKV + x) * P.max_seq + pp) * HD + 8 * (lane & 15);
+    }
+    case S_O:
+      return (const _Float16*)lw.o_proj_weight + (long)(HROWS * i + 2 * m + (lane >> 5)) * QSZ + OCOLS * x +
+             8 * (lane & 31);
+    case S_GU: {
+      const bool up = m >= 2 * GU_PER_WG;
+      const int mm = up ? m - 2 * GU_PER_WG : m;
+      const _Float16* W = (const _Float16*)(up ? lw.up_proj_weight : lw.gate_proj_weight);
+      return W + (long)(ICOLS * x + GU_PER_WG * i + (mm >> 1)) * HIDDEN + 512 * (mm & 1) + 8 * lane;
+    }
+    default: {  // S_DOWN: one 768-byte row segment per line; lanes 48-63 repeat lanes 0-15
+      const int ln = lane < 48 ? lane : lane - 48;
+      return (const _Float16*)lw.down_proj_weight + (long)(HROWS * i + m) * INTER + ICOLS * x + 8 * ln;
     }
   }
 }
 
-// Compute wave c of group c / 4 (member c % 4) runs the stages j with j % 2 == group.
-// Its single register buffer holds stage j's weights, loaded right after it computed
-// stage j - 2: the only loads in flight when it computes are the ones it needs, so the
-// compiler's wait for them never waits on a later prefetch.
-__device__ void compute_wave(const KParams& P, Shared* S, int c) {
-  const int w = blockIdx.x;
-  const int lane = __lane_id();
+__device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) {
+  Ctl C;
+  C.P = &P;
+  C.S = S;
+  C.r = ws_rsrc(P.ws);
+  C.ok = true;
+  C.deadline = P.deadline;
+  const int w = blockIdx.x, x = xcd_of(w), i = loc_of(w), lane = __lane_id();
   const int L = P.num_layers;
-  const int grp = c / NGW, m = c % NGW;
-  const int total = stages_per_token(P.mode, L) * P.num_steps;
-  const u64 deadline = 2 * P.deadline;
-  Buf b;
-  CState cs{-INFINITY, 0x7fffffff};
-  if (grp < total) prefetch(P, stage_desc(P.mode, L, grp), b, w, m, lane);
-  for (int j = grp; j < total; j += 2) {
-    const StageDesc d = stage_desc(P.mode, L, j);
-    if (!wait_ready(S, (u32)d.fin, deadline)) break;
-    const u32 fin_in_token = (u32)d.fin - (u32)(d.token * fins_per_token(P.mode, L));
-    if (m == 0) trace_mark(P, d.token, fin_in_token, TR_CSTART);
-    compute(P, S, d, b, cs, w, m, c, lane);
-    if (m == 0) trace_mark(P, d.token, fin_in_token, TR_CDONE);
-    if (j + 2 < total) prefetch(P, stage_desc(P.mode, L, j + 2), b, w, m, lane);
+  u32 gl = 0;
+  u32 phase = 0;
+  for (int t = 0; t < P.num_steps && C.ok; ++t) {
+    const int pos = P.start_pos + t, ctx = pos + 1;
+    if (P.mode != MODE_LMHEAD) {
+      u32 last = 0;  // last line issued
+      int pending = 0;  // lines issued whose completion is not yet published
+      const int nl = P.mode == MODE_MLP ? 1 : L;
+      const int s0 = P.mode == MODE_MLP ? 3 : 0;
+      for (int l = 0; l < nl && C.ok; ++l) {
+        for (int si = s0; si < 5 && C.ok; ++si) {
+          const int st = si == 0 ? S_QKV : (si == 1 ? S_ATT : (si == 2 ? S_O : (si == 3 ? S_GU : S_DOWN)));
+          const int nlines = stage_lines(st, ctx, i);
+          for (int m = (int)((u32)(q - (int)gl) & 3u); m < nlines; m += 4) {
+            const u32 n = gl + (u32)m;
+            // ring space: compute waves have released every line below n - RING_LINES + 1
+            u32 cmin = lds_ld(&S->cons[0]);
+#pragma unroll
+            for (int c = 1; c < NCW; ++c) cmin = min(cmin, lds_ld(&S->cons[c]));
+            if (n >= cmin + RING_LINES) {
+              // publish everything issued before waiting, so the compute waves can release lines
+              wait_vmcnt<0>();
+              if (pending > 0) lds_st(&S->done_upto[q], last + 4);
+              pending = 0;
+              const u64 t0 = wall_clock64();
+              int spins = 0;
+              for (;;) {
+                cmin = lds_ld(&S->cons[0]);
+#pragma unroll
+                for (int c = 1; c < NCW; ++c) cmin = min(cmin, lds_ld(&S->cons[c]));
+                if (n < cmin + RING_LINES) break;
+                if (give_up(C, t0, spins)) {
+                  C.ok = false;
+                  break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+              }
+              if (!C.ok) break;
+              lds_acquire();
+            }
+            dma16(line_src(P, S, st, l, m, x, i, pos, ctx, lane),
+                  __builtin_amdgcn_readfirstlane((u32)(n % RING_LINES) * LINE_BYTES));
+            last = n;
+            if (++pending > DMA_DEPTH) {
+              // all but the newest DMA_DEPTH lines of this wave are in LDS
+              wait_vmcnt<DMA_DEPTH>();
+              lds_st(&S->done_upto[q], n - 4 * DMA_DEPTH + 4);
+              pending = DMA_DEPTH;
+            }
+          }
+          gl += (u32)nlines;
+        }
+      }
+      wait_vmcnt<0>();
+      if (pending > 0) lds_st(&S->done_upto[q], last + 4);
+    }
+    if (P.mode == MODE_MLP) break;
+    ++phase;
+    lm_rows(C, P, NCW + q, t, phase);
   }
+  if (!C.ok) lds_st(&S->abort, 1u);
 }
 
 __global__ void __launch_bounds__(BLOCK, 1) qwen_decode_kernel(KParams P) {
   __shared__ Shared S;
   // wave index is uniform per wave; readfirstlane lets the compiler keep it (and
-  // every weight address derived from it) in scalar registers
+  // every address derived from it) in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   if (threadIdx.x == 0) {
-    S.ready = 0;
-    S.cnt[0] = 0;
-    S.cnt[1] = 0;
-    S.done[0] = 0;
-    S.done[1] = 0;
+    S.sync = 0;
+    S.xfin_cnt = 0;
+    S.lm_cnt = 0;
     S.abort = 0;
   }
+  if (threadIdx.x < NLW) S.done_upto[threadIdx.x] = threadIdx.x;
+  if (threadIdx.x < NCW) S.cons[threadIdx.x] = 0;
+  // (the isolated lm_head workload has no layers and passes no table)
+  if (P.mode != MODE_LMHEAD && threadIdx.x < P.num_layers * 12) {
+    const u64* src = (const u64*)P.layers;
+    ((u64*)S.lw)[threadIdx.x] = src[threadIdx.x];
+  }
   __syncthreads();
-  if (wave == NCW)
-    exchange_wave(P, &S);
-  else
+  if (wave < NCW)
     compute_wave(P, &S, wave);
+  else
+    loader_wave(P, &S, wave - NCW);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1262,8 +1360,9 @@ int fill_decode(KParams& P, const void* embed, const LDGLayerWeight* lw, const v
   if (!aligned16(lw) || !aligned16(embed) || !aligned16(lm_head) || !aligned16(kc) || !aligned16(vc) ||
       !aligned16(cos_t) || !aligned16(sin_t) || !aligned16(hidden) || !aligned16(norm_out) || !aligned16(fnorm))
     return QWEN_ERR_ARG;
-  if (num_layers < 1 || num_layers > MAX_LAYERS || steps < 1 || start < 0 || max_seq < 1 ||
-      (long)start + steps > (long)max_seq || max_seq > NSPLIT * MAX_SPLIT_POS)
+  // max_seq must keep every ring line of 4 positions inside the cache
+  if (num_layers < 1 || num_layers > MAX_LAYERS || steps < 1 || start < 0 || max_seq < 4 || (max_seq & 3) != 0 ||
+      (long)start + steps > (long)max_seq || max_seq > MAX_SEQ_LIMIT)
     return QWEN_ERR_ARG;
   memset(&P, 0, sizeof(P));
   P.embed = (const _Float16*)embed;
@@ -1364,6 +1463,7 @@ extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, i
   P.mode = MODE_LMHEAD;
   P.num_layers = 1;
   P.num_steps = 1;
+  P.max_seq = MAX_SEQ_LIMIT;
   return launch(P, stream);
 }
 
@@ -1397,6 +1497,7 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
   P.mode = MODE_MLP;
   P.num_layers = 1;
   P.num_steps = 1;
+  P.max_seq = MAX_SEQ_LIMIT;
   return launch(P, stream);
 }
 
