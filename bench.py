@@ -101,7 +101,7 @@ def main():
                          "run can scale FETCH_SIZE / WRITE_SIZE against a kernel of known traffic")
     ap.add_argument("--trace", default=None,
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
-                         "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, 4 events], 100 MHz ticks)")
+                         "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, events], 100 MHz ticks)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine runs one sequence on one MI355X; --gpus {args.gpus} "

@@ -266,6 +266,66 @@ int main() {
     for (int r = 0; r < HIDDEN * NXCD; ++r) CHECK(rows[r] == 1, "down row %d", r);
   }
 
+  // ---- loader streams: every line / lane element equals the per-line row-column formula ----
+  {
+    const long msize[9] = {(long)QSZ * HIDDEN, (long)KVSZ * HIDDEN, (long)KVSZ * HIDDEN, 0, 0,
+                           (long)HIDDEN * QSZ, (long)INTER * HIDDEN, (long)INTER * HIDDEN, (long)HIDDEN * INTER};
+    const int max_seq = MAX_SEQ_LIMIT;
+    const int ctxs[] = {1, 2, 3, 4, 5, 31, 127, 128, 129, 500, 1021, 1920, 1921, 2000, 2047, 2048};
+    for (int ctx : ctxs) {
+      const int pos = ctx - 1;
+      for (int x = 0; x < NXCD; ++x)
+        for (int i = 0; i < NLOC; ++i) {
+          int total = 0;
+          for (int si = 0; si < NSTREAM; ++si)
+            for (int lane = 0; lane < WAVE; ++lane) {
+              const StreamGeom g = stream_geom(si, x, i, ctx, pos, max_seq, lane);
+              if (lane == 0) total += g.n;
+              for (int m = 0; m < g.n; ++m) {
+                const long e = g.elem0 + m * g.stride + g.loff;
+                long want = -1;
+                int want_mat = g.mat;
+                switch (si) {
+                  case 0: {
+                    const int gr = QKV_PER_WG * i + (m >> 1);
+                    want_mat = grp_matrix(gr);
+                    want = (long)grp_row_in(x, gr) * HIDDEN + 512 * (m & 1) + 8 * lane;
+                    break;
+                  }
+                  case 1:
+                  case 2: {
+                    const int p = att_t0(ctx, i) + 4 * m + (lane >> 4);
+                    const bool cached = 4 * m + (lane >> 4) < g.vlim;
+                    const int lim = att_t1(ctx, i) < pos ? att_t1(ctx, i) : pos;
+                    CHECK(cached == (p < lim), "K/V cached lanes ctx %d", ctx);
+                    if (!cached) continue;
+                    CHECK(p >= 0 && p < pos && p < max_seq, "K/V position");
+                    want = (long)p * HD + 8 * (lane & 15);
+                    CHECK(e + 8 <= (long)max_seq * HD, "K/V element range");
+                    break;
+                  }
+                  case 3:
+                    want = (long)(HROWS * i + 2 * m + (lane >> 5)) * QSZ + OCOLS * x + 8 * (lane & 31);
+                    break;
+                  case 4:
+                  case 5:
+                    want = (long)(ICOLS * x + GU_PER_WG * i + (m >> 1)) * HIDDEN + 512 * (m & 1) + 8 * lane;
+                    break;
+                  default:
+                    want = (long)(HROWS * i + m) * INTER + ICOLS * x + 8 * (lane < 48 ? lane : lane - 48);
+                    break;
+                }
+                CHECK(want_mat == g.mat && e == want, "stream %d element x%d i%d m%d lane%d", si, x, i, m, lane);
+                if (g.mat != 3 && g.mat != 4) CHECK(e >= 0 && e + 8 <= msize[g.mat], "stream %d in matrix", si);
+              }
+            }
+          int st_total = 0;
+          for (int st = 0; st < NSTAGE; ++st) st_total += stage_lines(st, ctx, i);
+          CHECK(total == st_total, "streams cover the stage lines ctx %d", ctx);
+        }
+    }
+  }
+
   // ---- ring schedule: every stage fits the ring ----
   for (int ctx = 1; ctx <= MAX_SEQ_LIMIT; ++ctx)
     for (int s = 0; s < NSPLIT; ++s)

@@ -56,12 +56,14 @@ constexpr u32 ST_TIMEOUT = 1u;
 constexpr u32 ST_BAD_TOKEN = 2u;
 constexpr int DMA_DEPTH = 16;  // LDS-DMA lines a loader wave keeps in flight
 // optional device timestamps (wall clock) per workgroup and stage of one token
-constexpr int TRACE_EVENTS = 4;
+constexpr int TRACE_EVENTS = 6;
 enum TraceEvent : int {
   TR_POLL = 0,   // compute wave 0 starts waiting for the stage input
   TR_INPUT = 1,  // compute wave 0 has its quarter of the input
   TR_SYNC = 2,   // compute wave 0 passed the compute-wave barrier (whole input in LDS)
   TR_STORE = 3,  // compute wave 0 stored its results
+  TR_LINES = 4,  // compute wave 0 has the stage's weight / K-V lines in the ring
+  TR_MERGE = 5,  // attention: compute wave 0 passed the barrier before the split merge
 };
 QL_HD int trace_stages(int L) { return NSTAGE * L + 1; }
 
@@ -224,8 +226,16 @@ __device__ __forceinline__ u32 pack_h2(float a, float b) {
 __device__ __forceinline__ float lo_h(u32 p) { return (float)__builtin_bit_cast(h2, p)[0]; }
 __device__ __forceinline__ float hi_h(u32 p) { return (float)__builtin_bit_cast(h2, p)[1]; }
 
+// a slot read by workgroups on other XCDs: device-scope (sc1) store
 __device__ __forceinline__ void ll_store(u64* ws, long slot, u32 payload, u32 tag) {
   __hip_atomic_store(ws + slot, ((u64)tag << 32) | (u64)payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// a slot read only by workgroups of the writer's XCD: a plain 8-byte store lands in
+// the XCD's L2, where the readers' device-scope loads find it (measured on MI355X:
+// a 32-workgroup all-gather of 1024 values takes 1.1 us per round this way, 1.5 us
+// with device-scope stores)
+__device__ __forceinline__ void ll_store_xcd(u64* ws, long slot, u32 payload, u32 tag) {
+  __hip_atomic_store(ws + slot, ((u64)tag << 32) | (u64)payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const u64* ws) {
@@ -564,6 +574,7 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   const u32 n0 = W.gl;
   W.gl += LINES_QKV;
   wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
   float part[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + 2 * (4 * W.c + r), lane, a, b);
@@ -572,7 +583,7 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   const float rs = reduce4(part[0], part[1], part[2], part[3]);
   const float r0 = bcast(rs, 0), r1 = bcast(rs, 32), r2 = bcast(rs, 16), r3 = bcast(rs, 48);
   if (lane < 2)
-    ll_store(P.ws, xbuf(par, W.x, B_QKV) + (QKV_PER_WG / 2) * W.i + 2 * W.c + lane,
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_QKV) + (QKV_PER_WG / 2) * W.i + 2 * W.c + lane,
              lane == 0 ? pack_h2(r0, r1) : pack_h2(r2, r3), tag_of(epoch, l, S_QKV));
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_STORE);
   W.par_in ^= 1;
@@ -647,51 +658,41 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   const u32 n0 = W.gl;
   W.gl += 2 * nk;
   const int j = lane >> 4, q16 = lane & 15;
-  float qa[8], qb[8], kc[8], vc[8];
+  float qa[8], qb[8];
   {
     const float4 a0 = *(const float4*)(S->qr + 8 * q16), a1 = *(const float4*)(S->qr + 8 * q16 + 4);
     const float4 b0 = *(const float4*)(S->qr + 128 + 8 * q16), b1 = *(const float4*)(S->qr + 128 + 8 * q16 + 4);
-    const float4 k0 = *(const float4*)(S->qr + 256 + 8 * q16), k1 = *(const float4*)(S->qr + 256 + 8 * q16 + 4);
-    const float4 v0 = *(const float4*)(S->qr + 384 + 8 * q16), v1 = *(const float4*)(S->qr + 384 + 8 * q16 + 4);
-    const float aa[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qa[e] = aa[e];
-      qb[e] = bb[e];
-      kc[e] = (float)(_Float16)kk[e];  // the current position's k and v as the cache holds them
-      vc[e] = (float)(_Float16)vv[e];
-    }
+    qa[0] = a0.x; qa[1] = a0.y; qa[2] = a0.z; qa[3] = a0.w; qa[4] = a1.x; qa[5] = a1.y; qa[6] = a1.z; qa[7] = a1.w;
+    qb[0] = b0.x; qb[1] = b0.y; qb[2] = b0.z; qb[3] = b0.w; qb[4] = b1.x; qb[5] = b1.y; qb[6] = b1.z; qb[7] = b1.w;
   }
   wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
+  // the current position is not in the cache lines (the loader reads a spare row for it):
+  // the wave whose 16 positions include it writes its fp16 k and v into its own ring lines
+  {
+    const int mp = (pos - t0) >> 2, jp = (pos - t0) & 3;
+    if (pos >= t0 && pos < t1 && (mp >> 2) == W.c && j == jp) {
+      const float4 k0 = *(const float4*)(S->qr + 256 + 8 * q16), k1 = *(const float4*)(S->qr + 256 + 8 * q16 + 4);
+      const float4 v0 = *(const float4*)(S->qr + 384 + 8 * q16), v1 = *(const float4*)(S->qr + 384 + 8 * q16 + 4);
+      const h8 kh = {(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w,
+                     (_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
+      const h8 vh = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
+                     (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
+      S->ring[(n0 + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, kh);
+      S->ring[(n0 + nk + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, vh);
+    }
+  }
   float sc[4][2];
-  bool valid[4], cur[4];
+  bool valid[4];
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
     const int m = 4 * W.c + bb;
-    const int pp = t0 + 4 * m + j;
-    valid[bb] = m < nk && pp < t1;
-    cur[bb] = pp == pos;
+    valid[bb] = m < nk && t0 + 4 * m + j < t1;
     float s0 = 0.f, s1 = 0.f;
     if (m < nk) {
-      float kf[8];
-      if (cur[bb]) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] = kc[e];
-      } else {
-        const h8 kh = __builtin_bit_cast(h8, ring_line(S, n0 + m)[lane]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] = (float)kh[e];
-      }
-      s0 = kf[0] * qa[0];
-      s1 = kf[0] * qb[0];
-#pragma unroll
-      for (int e = 1; e < 8; ++e) {
-        s0 = fmaf(kf[e], qa[e], s0);
-        s1 = fmaf(kf[e], qb[e], s1);
-      }
+      const v4u kw = ring_line(S, n0 + m)[lane];
+      s0 = dot8(kw, qa);
+      s1 = dot8(kw, qb);
     }
     s0 = row16_sum(s0) * P.attn_scale;
     s1 = row16_sum(s1) * P.attn_scale;
@@ -699,39 +700,37 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     sc[bb][1] = valid[bb] ? s1 : -INFINITY;
   }
   float mh[2], lh[2], acc[2][8];
+  float pr[2][4];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float mx = rows4_max(fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h])));
     mh[h] = mx;
-    float pr[4], lsum = 0.f;
+    float lsum = 0.f;
 #pragma unroll
     for (int bb = 0; bb < 4; ++bb) {
-      pr[bb] = valid[bb] ? __expf(sc[bb][h] - mx) : 0.f;
-      lsum += pr[bb];
+      pr[h][bb] = valid[bb] ? __expf(sc[bb][h] - mx) : 0.f;
+      lsum += pr[h][bb];
     }
     lh[h] = rows4_sum(lsum);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-      const int m = 4 * W.c + bb;
-      if (m < nk) {
-        float vf[8];
-        if (cur[bb]) {
+  for (int bb = 0; bb < 4; ++bb) {
+    const int m = 4 * W.c + bb;
+    if (m < nk) {
+      const h8 vh = __builtin_bit_cast(h8, ring_line(S, n0 + nk + m)[lane]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = vc[e];
-        } else {
-          const h8 vh = __builtin_bit_cast(h8, ring_line(S, n0 + nk + m)[lane]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = (float)vh[e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(pr[bb], vf[e], acc[h][e]);
+      for (int e = 0; e < 8; ++e) {
+        acc[0][e] = fmaf(pr[0][bb], (float)vh[e], acc[0][e]);
+        acc[1][e] = fmaf(pr[1][bb], (float)vh[e], acc[1][e]);
       }
     }
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[h][e] = rows4_sum(acc[h][e]);
-  }
   release_lines(W, W.gl);
   float* rec = &S->apart[W.c][0][0];
   if (lane < 16) {
@@ -748,6 +747,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     rec[PART_PER_HEAD + 1] = lh[1];
   }
   sync4(W);
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_MERGE);
   // merge the 4 wave partials: wave c writes entries [65 c, 65 c + 65) of the 260
   float Mx[2], wt[2][NCW];
 #pragma unroll
@@ -775,7 +775,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
 #pragma unroll
         for (int cc = 0; cc < NCW; ++cc) val = fmaf(h ? wt[1][cc] : wt[0][cc], S->apart[cc][h][k], val);
       }
-      ll_store(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
+      ll_store_xcd(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
     }
   }
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
@@ -816,7 +816,7 @@ __device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u
   const float oa = lane == 0 ? o[0] : (lane == 1 ? o[2] : (lane == 2 ? o[4] : o[6]));
   const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
   if (lane < 4)
-    ll_store(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + lane, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + lane, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
   trace_ev(P, t, NSTAGE * l + S_COMB, TR_STORE);
 }
 
@@ -844,6 +844,7 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   const u32 n0 = W.gl;
   W.gl += LINES_O;
   wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
   // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
   float part[4];
 #pragma unroll
@@ -905,7 +906,7 @@ __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u3
         P.out_vec[HROWS * W.i + r + 1] = s1;
       }
     } else {
-      ll_store(P.ws, xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 4 * W.c + lane, pack_h2(s0, s1),
+      ll_store_xcd(P.ws, xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 4 * W.c + lane, pack_h2(s0, s1),
                tag_of(epoch, l, st));
       if (is_down && l == P.num_layers - 1 && W.x == 0) {  // final-layer residual
         const int row = HROWS * W.i + r;
@@ -947,6 +948,7 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   const u32 n0 = W.gl;
   W.gl += LINES_GU;
   wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
   float part[6];
 #pragma unroll
   for (int jj = 0; jj < 3; ++jj) {
@@ -962,7 +964,7 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   const float s1 = g1 / (1.0f + __expf(-g1)) * u1;
   const float s2 = g2 / (1.0f + __expf(-g2)) * u2;
   if (lane < 2)
-    ll_store(P.ws, xbuf(par, W.x, B_INT) + int_slot(W.i, W.c, lane), lane == 0 ? pack_h2(s0, s1) : pack_h2(s2, 0.f),
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_INT) + int_slot(W.i, W.c, lane), lane == 0 ? pack_h2(s0, s1) : pack_h2(s2, 0.f),
              tag_of(epoch, l, S_GU));
   trace_ev(P, t, NSTAGE * l + S_GU, TR_STORE);
   W.par_in ^= 1;
@@ -999,6 +1001,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   const u32 n0 = W.gl;
   W.gl += LINES_DOWN;
   wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
   float part[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) part[r] = dot8(ring_line(S, n0 + 8 * W.c + r)[lane], a);
@@ -1130,45 +1133,42 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
 
 // ------------------------------------------------------------------------------------
 // loader waves: every ring line of every stage in execution order; wave q
-// handles the lines n == q (mod 4). The address of lane `lane`'s 16 bytes of
-// line m of a stage:
+// handles the lines n == q (mod 4). Each stage is one or two streams of lines
+// whose 16-byte piece for lane `lane` is at base + m * stride + loff: the
+// weight rows a workgroup reads are contiguous per stage (QKV: 16 rows of one
+// matrix; gate, up: 12 rows each) or evenly strided (o_proj: 2 rows of 512 B
+// per line; down: one 768-byte row segment per line), and 4 positions of one
+// kv head are 1 KB of contiguous K (or V) cache.
 
-__device__ __forceinline__ const void* line_src(const KParams& P, const Shared* S, int st, int l, int m, int x, int i,
-                                                int pos, int ctx, int lane) {
+struct Stream {
+  const char* base;  // this lane's first byte of line 0
+  long stride;       // bytes between lines
+  int n;             // lines
+  int vlim;          // K/V streams: lane's position index 4 m + lane / 16 must be < vlim
+};
+
+__device__ __forceinline__ Stream make_stream(const KParams& P, const Shared* S, int si, int l, int x, int i, int pos,
+                                              int ctx, int lane) {
   const LDGLayerWeight& lw = S->lw[l];
-  switch (st) {
-    case S_QKV: {
-      const int gr = QKV_PER_WG * i + (m >> 1);
-      const int mat = grp_matrix(gr);
-      const _Float16* W = (const _Float16*)(mat == 0 ? lw.q_proj_weight : (mat == 1 ? lw.k_proj_weight : lw.v_proj_weight));
-      return W + (long)grp_row_in(x, gr) * HIDDEN + 512 * (m & 1) + 8 * lane;
-    }
-    case S_ATT: {
-      const int nk = att_nk(ctx, i), t0 = att_t0(ctx, i), t1 = att_t1(ctx, i);
-      const bool is_v = m >= nk;
-      const int mm = is_v ? m - nk : m;
-      const int pp = t0 + 4 * mm + (lane >> 4);
-      const int lim = t1 < pos ? t1 : pos;  // positions already in the cache
-      // lanes without a cached position read the embedding's first row instead, so the
-      // DMA always covers all 64 lanes and no line of an unwritten position is cached
-      if (pp >= lim) return P.embed + 8 * lane;
-      const _Float16* base = is_v ? P.v_cache : P.k_cache;
-      return base + (((long)l * NKV + x) * P.max_seq + pp) * HD + 8 * (lane & 15);
-    }
-    case S_O:
-      return (const _Float16*)lw.o_proj_weight + (long)(HROWS * i + 2 * m + (lane >> 5)) * QSZ + OCOLS * x +
-             8 * (lane & 31);
-    case S_GU: {
-      const bool up = m >= 2 * GU_PER_WG;
-      const int mm = up ? m - 2 * GU_PER_WG : m;
-      const _Float16* W = (const _Float16*)(up ? lw.up_proj_weight : lw.gate_proj_weight);
-      return W + (long)(ICOLS * x + GU_PER_WG * i + (mm >> 1)) * HIDDEN + 512 * (mm & 1) + 8 * lane;
-    }
-    default: {  // S_DOWN: one 768-byte row segment per line; lanes 48-63 repeat lanes 0-15
-      const int ln = lane < 48 ? lane : lane - 48;
-      return (const _Float16*)lw.down_proj_weight + (long)(HROWS * i + m) * INTER + ICOLS * x + 8 * ln;
-    }
-  }
+  const StreamGeom g = stream_geom(si, x, i, ctx, pos, P.max_seq, lane);
+  const void* mats[9] = {lw.q_proj_weight, lw.k_proj_weight, lw.v_proj_weight,
+                         P.k_cache + ((long)l * NKV + x) * P.max_seq * HD, P.v_cache + ((long)l * NKV + x) * P.max_seq * HD,
+                         lw.o_proj_weight, lw.gate_proj_weight, lw.up_proj_weight, lw.down_proj_weight};
+  const _Float16* M = (const _Float16*)(g.mat == 0 ? mats[0] : g.mat == 1 ? mats[1] : g.mat == 2 ? mats[2]
+                                        : g.mat == 3 ? mats[3] : g.mat == 4 ? mats[4] : g.mat == 5 ? mats[5]
+                                        : g.mat == 6 ? mats[6] : g.mat == 7 ? mats[7] : mats[8]);
+  Stream st;
+  st.base = (const char*)(M + g.elem0 + g.loff);
+  st.stride = g.stride * 2;
+  st.n = g.n;
+  st.vlim = g.vlim;
+  return st;
+}
+
+__device__ __forceinline__ u32 cons_min(const Shared* S) {
+  const u32 a = lds_ld(&S->cons[0]), b = lds_ld(&S->cons[1]);
+  const u32 c = lds_ld(&S->cons[2]), d = lds_ld(&S->cons[3]);
+  return min(min(a, b), min(c, d));
 }
 
 __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) {
@@ -1180,48 +1180,49 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
   C.deadline = P.deadline;
   const int w = blockIdx.x, x = xcd_of(w), i = loc_of(w), lane = __lane_id();
   const int L = P.num_layers;
-  u32 gl = 0;
+  // lanes without a cached position read the embedding's first row instead, so every
+  // DMA covers all 64 lanes and no line of an unwritten position is ever cached
+  const char* spare = (const char*)P.embed + 16 * lane;
+  u32 gl = 0;     // global index of the next stream's first line
+  u32 avail = 0;  // lines below this may be written (compute waves released their slots)
   u32 phase = 0;
   for (int t = 0; t < P.num_steps && C.ok; ++t) {
     const int pos = P.start_pos + t, ctx = pos + 1;
     if (P.mode != MODE_LMHEAD) {
-      u32 last = 0;  // last line issued
+      u32 last = 0;     // last line issued
       int pending = 0;  // lines issued whose completion is not yet published
       const int nl = P.mode == MODE_MLP ? 1 : L;
-      const int s0 = P.mode == MODE_MLP ? 3 : 0;
+      const int s0 = P.mode == MODE_MLP ? 4 : 0;
       for (int l = 0; l < nl && C.ok; ++l) {
-        for (int si = s0; si < 5 && C.ok; ++si) {
-          const int st = si == 0 ? S_QKV : (si == 1 ? S_ATT : (si == 2 ? S_O : (si == 3 ? S_GU : S_DOWN)));
-          const int nlines = stage_lines(st, ctx, i);
-          for (int m = (int)((u32)(q - (int)gl) & 3u); m < nlines; m += 4) {
+        for (int si = s0; si < 7 && C.ok; ++si) {
+          const Stream st = make_stream(P, S, si, l, x, i, pos, ctx, lane);
+          const char* src = st.base;
+          int m = (int)((u32)(q - (int)gl) & 3u);
+          src += (long)m * st.stride;
+          for (; m < st.n; m += 4, src += 4 * st.stride) {
             const u32 n = gl + (u32)m;
-            // ring space: compute waves have released every line below n - RING_LINES + 1
-            u32 cmin = lds_ld(&S->cons[0]);
-#pragma unroll
-            for (int c = 1; c < NCW; ++c) cmin = min(cmin, lds_ld(&S->cons[c]));
-            if (n >= cmin + RING_LINES) {
-              // publish everything issued before waiting, so the compute waves can release lines
-              wait_vmcnt<0>();
-              if (pending > 0) lds_st(&S->done_upto[q], last + 4);
-              pending = 0;
-              const u64 t0 = wall_clock64();
-              int spins = 0;
-              for (;;) {
-                cmin = lds_ld(&S->cons[0]);
-#pragma unroll
-                for (int c = 1; c < NCW; ++c) cmin = min(cmin, lds_ld(&S->cons[c]));
-                if (n < cmin + RING_LINES) break;
-                if (give_up(C, t0, spins)) {
-                  C.ok = false;
-                  break;
+            if (n >= avail) {
+              avail = cons_min(S) + RING_LINES;
+              if (n >= avail) {
+                // publish everything issued before waiting, so the compute waves can release lines
+                wait_vmcnt<0>();
+                if (pending > 0) lds_st(&S->done_upto[q], last + 4);
+                pending = 0;
+                const u64 t0 = wall_clock64();
+                int spins = 0;
+                while (n >= (avail = cons_min(S) + RING_LINES)) {
+                  if (give_up(C, t0, spins)) {
+                    C.ok = false;
+                    break;
+                  }
+                  __builtin_amdgcn_s_sleep(1);
                 }
-                __builtin_amdgcn_s_sleep(1);
+                if (!C.ok) break;
+                lds_acquire();
               }
-              if (!C.ok) break;
-              lds_acquire();
             }
-            dma16(line_src(P, S, st, l, m, x, i, pos, ctx, lane),
-                  __builtin_amdgcn_readfirstlane((u32)(n % RING_LINES) * LINE_BYTES));
+            const bool cached = 4 * m + (lane >> 4) < st.vlim;
+            dma16(cached ? src : spare, __builtin_amdgcn_readfirstlane((n % RING_LINES) * LINE_BYTES));
             last = n;
             if (++pending > DMA_DEPTH) {
               // all but the newest DMA_DEPTH lines of this wave are in LDS
@@ -1230,7 +1231,7 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
               pending = DMA_DEPTH;
             }
           }
-          gl += (u32)nlines;
+          gl += (u32)st.n;
         }
       }
       wait_vmcnt<0>();

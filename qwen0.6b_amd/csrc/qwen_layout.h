@@ -108,6 +108,68 @@ QL_HD int stage_lines(int st, int ctx, int s) {
 // stages of a layer in execution order; MLP mode runs GU..DSUM only
 QL_HD int first_stage(int mode) { return mode == MODE_MLP ? S_GU : S_QKV; }
 
+// ---- loader streams ------------------------------------------------------------------
+// The ring lines of a layer come from 7 streams, in this order: 0 QKV (32 lines),
+// 1 K (nk), 2 V (nk), 3 o_proj (16), 4 gate (24), 5 up (24), 6 down (32). Line m
+// of a stream gives lane `lane` 8 fp16 values at element
+//   elem0 + m * stride + loff
+// of the stream's matrix (mat: 0..2 = Wq/Wk/Wv, 3 K cache, 4 V cache, 5 Wo,
+// 6 Wg, 7 Wu, 8 Wd; cache elements counted from layer l's kv head x at position
+// 0). For K/V lines, lanes whose position index 4 m + lane / 16 is >= vlim
+// read no cache element (they read a fixed spare row instead).
+constexpr int NSTREAM = 7;
+struct StreamGeom {
+  int mat;
+  long elem0, stride, loff;
+  int n, vlim;
+};
+QL_HD StreamGeom stream_geom(int si, int x, int i, int ctx, int pos, int max_seq, int lane) {
+  StreamGeom g;
+  g.vlim = 0x7fffffff;
+  g.loff = 8 * lane;
+  g.stride = 512;
+  switch (si) {
+    case 0: {
+      const int gr = QKV_PER_WG * i;
+      g.mat = grp_matrix(gr);
+      g.elem0 = (long)grp_row_in(x, gr) * HIDDEN;
+      g.n = LINES_QKV;
+      break;
+    }
+    case 1:
+    case 2: {
+      const int t0 = att_t0(ctx, i), t1 = att_t1(ctx, i);
+      g.mat = si == 1 ? 3 : 4;
+      g.elem0 = (long)t0 * HD;
+      g.n = att_nk(ctx, i);
+      g.vlim = (t1 < pos ? t1 : pos) - t0;
+      (void)max_seq;
+      break;
+    }
+    case 3:
+      g.mat = 5;
+      g.elem0 = (long)HROWS * i * QSZ + OCOLS * x;
+      g.stride = 2L * QSZ;
+      g.loff = (long)(lane >> 5) * QSZ + 8 * (lane & 31);
+      g.n = LINES_O;
+      break;
+    case 4:
+    case 5:
+      g.mat = si == 4 ? 6 : 7;
+      g.elem0 = (long)(ICOLS * x + GU_PER_WG * i) * HIDDEN;
+      g.n = 2 * GU_PER_WG;
+      break;
+    default:
+      g.mat = 8;
+      g.elem0 = (long)HROWS * i * INTER + ICOLS * x;
+      g.stride = INTER;
+      g.loff = 8 * (lane < 48 ? lane : lane - 48);
+      g.n = LINES_DOWN;
+      break;
+  }
+  return g;
+}
+
 // ---- LM head ------------------------------------------------------------------------
 constexpr int LM_BASE = VOCAB / NWG;        // 593
 constexpr int LM_EXTRA = VOCAB % NWG;       // 128
