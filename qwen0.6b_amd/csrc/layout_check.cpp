@@ -66,7 +66,7 @@ int main() {
     for (int r = 0; r < QSZ; ++r) CHECK(q[r] == 1, "q row %d seen %d", r, q[r]);
     for (int r = 0; r < KVSZ; ++r) CHECK(k[r] == 1 && v[r] == 1, "k/v row %d", r);
     // ring lines of the QKV stage: line m = row m / 2, half m % 2
-    for (int m = 0; m < LINES_QKV; ++m) CHECK((m >> 1) < QKV_PER_WG, "qkv line");
+    for (int m = 0; m < LINES_QKV - LINES_NORM; ++m) CHECK((m >> 1) < QKV_PER_WG, "qkv line");
   }
 
   // ---- attention input poll: quarter c, lane < 32 -> values 4 (32 c + lane) .. +4 ----
@@ -231,7 +231,7 @@ int main() {
     std::vector<int> g(INTER, 0);
     for (int x = 0; x < NXCD; ++x)
       for (int i = 0; i < NLOC; ++i)
-        for (int m = 0; m < LINES_GU; ++m) {
+        for (int m = 0; m < LINES_GU - LINES_NORM; ++m) {
           const bool up = m >= 2 * GU_PER_WG;
           const int mm = up ? m - 2 * GU_PER_WG : m;
           const int row = ICOLS * x + GU_PER_WG * i + (mm >> 1);
@@ -241,7 +241,7 @@ int main() {
     for (int r = 0; r < INTER; ++r) CHECK(g[r] == 1, "gate row %d", r);
     // compute wave c: gate rows 3c + jj at lines 2(3c + jj), up at 24 + 2(3c + jj)
     for (int c = 0; c < NCW; ++c)
-      for (int jj = 0; jj < 3; ++jj) CHECK(2 * GU_PER_WG + 2 * (3 * c + jj) + 1 < LINES_GU, "gu lines");
+      for (int jj = 0; jj < 3; ++jj) CHECK(LINES_NORM + 2 * GU_PER_WG + 2 * (3 * c + jj) + 1 < LINES_GU, "gu lines");
     // INT slots and the down poll: pair k = 32 c + lane -> values 12 (k/4) + 3 (k%4) + {0,1,2}
     std::vector<int> seen(ICOLS, 0);
     for (int c = 0; c < NCW; ++c)
@@ -268,32 +268,47 @@ int main() {
 
   // ---- loader streams: every line / lane element equals the per-line row-column formula ----
   {
-    const long msize[9] = {(long)QSZ * HIDDEN, (long)KVSZ * HIDDEN, (long)KVSZ * HIDDEN, 0, 0,
-                           (long)HIDDEN * QSZ, (long)INTER * HIDDEN, (long)INTER * HIDDEN, (long)HIDDEN * INTER};
+    // element counts of the sources (K/V: one kv head of one layer)
     const int max_seq = MAX_SEQ_LIMIT;
+    const long msize[15] = {(long)QSZ * HIDDEN, (long)KVSZ * HIDDEN, (long)KVSZ * HIDDEN, (long)max_seq * HD,
+                            (long)max_seq * HD, (long)HIDDEN * QSZ, (long)INTER * HIDDEN, (long)INTER * HIDDEN,
+                            (long)HIDDEN * INTER, HIDDEN, HIDDEN, HD, HD, (long)max_seq * HD, (long)max_seq * HD};
     const int ctxs[] = {1, 2, 3, 4, 5, 31, 127, 128, 129, 500, 1021, 1920, 1921, 2000, 2047, 2048};
     for (int ctx : ctxs) {
       const int pos = ctx - 1;
       for (int x = 0; x < NXCD; ++x)
         for (int i = 0; i < NLOC; ++i) {
-          int total = 0;
+          int total = 0, mlp_total = 0;
           for (int si = 0; si < NSTREAM; ++si)
             for (int lane = 0; lane < WAVE; ++lane) {
-              const StreamGeom g = stream_geom(si, x, i, ctx, pos, max_seq, lane);
-              if (lane == 0) total += g.n;
+              const StreamGeom g = stream_geom(si, x, i, ctx, pos, lane);
+              if (lane == 0) {
+                total += g.n;
+                if (si >= MLP_FIRST_STREAM) mlp_total += g.n;
+              }
               for (int m = 0; m < g.n; ++m) {
                 const long e = g.elem0 + m * g.stride + g.loff;
                 long want = -1;
-                int want_mat = g.mat;
+                int want_mat = -1;
                 switch (si) {
-                  case 0: {
+                  case 0:
+                  case 6:
+                    want_mat = si == 0 ? 9 : 10;
+                    want = 512 * m + 8 * lane;
+                    break;
+                  case 1: {
                     const int gr = QKV_PER_WG * i + (m >> 1);
                     want_mat = grp_matrix(gr);
                     want = (long)grp_row_in(x, gr) * HIDDEN + 512 * (m & 1) + 8 * lane;
                     break;
                   }
-                  case 1:
-                  case 2: {
+                  case 2:
+                    want_mat = 11 + (lane >> 4);
+                    want = ((lane >> 4) >= 2 ? (long)pos * HD : 0) + 8 * (lane & 15);
+                    break;
+                  case 3:
+                  case 4: {
+                    want_mat = si == 3 ? 3 : 4;
                     const int p = att_t0(ctx, i) + 4 * m + (lane >> 4);
                     const bool cached = 4 * m + (lane >> 4) < g.vlim;
                     const int lim = att_t1(ctx, i) < pos ? att_t1(ctx, i) : pos;
@@ -301,28 +316,39 @@ int main() {
                     if (!cached) continue;
                     CHECK(p >= 0 && p < pos && p < max_seq, "K/V position");
                     want = (long)p * HD + 8 * (lane & 15);
-                    CHECK(e + 8 <= (long)max_seq * HD, "K/V element range");
                     break;
                   }
-                  case 3:
+                  case 5:
+                    want_mat = 5;
                     want = (long)(HROWS * i + 2 * m + (lane >> 5)) * QSZ + OCOLS * x + 8 * (lane & 31);
                     break;
-                  case 4:
-                  case 5:
+                  case 7:
+                  case 8:
+                    want_mat = si == 7 ? 6 : 7;
                     want = (long)(ICOLS * x + GU_PER_WG * i + (m >> 1)) * HIDDEN + 512 * (m & 1) + 8 * lane;
                     break;
                   default:
+                    want_mat = 8;
                     want = (long)(HROWS * i + m) * INTER + ICOLS * x + 8 * (lane < 48 ? lane : lane - 48);
                     break;
                 }
                 CHECK(want_mat == g.mat && e == want, "stream %d element x%d i%d m%d lane%d", si, x, i, m, lane);
-                if (g.mat != 3 && g.mat != 4) CHECK(e >= 0 && e + 8 <= msize[g.mat], "stream %d in matrix", si);
+                CHECK(g.mat >= 0 && g.mat < 15 && e >= 0 && e + 8 <= msize[g.mat], "stream %d in its source", si);
               }
             }
           int st_total = 0;
           for (int st = 0; st < NSTAGE; ++st) st_total += stage_lines(st, ctx, i);
           CHECK(total == st_total, "streams cover the stage lines ctx %d", ctx);
+          CHECK(mlp_total == stage_lines(S_GU, ctx, i) + stage_lines(S_DOWN, ctx, i), "MLP streams");
         }
+    }
+    // stage-by-stage: the stream line counts add up to each stage's lines, in order
+    for (int ctx : ctxs) {
+      const int pos = ctx - 1;
+      const int sl[NSTREAM] = {0, 0, 1, 1, 1, 3, 5, 5, 5, 6};  // stage of each stream
+      int per_stage[NSTAGE] = {0};
+      for (int si = 0; si < NSTREAM; ++si) per_stage[sl[si]] += stream_geom(si, 0, 5, ctx, pos, 0).n;
+      for (int st = 0; st < NSTAGE; ++st) CHECK(per_stage[st] == stage_lines(st, ctx, 5), "stage %d lines", st);
     }
   }
 

@@ -372,6 +372,16 @@ __device__ __forceinline__ void lds_wait_ge(Ctl& C, const u32* p, u32 v) {
   lds_acquire();
 }
 
+// Each compute wave waits for its own result stores before it starts polling the next stage's
+// inputs. Polls issued while the stores are still in flight delay those stores (the consumer's
+// hop grows by about 0.5 us per stage); bit s of the mask enables this after stage s.
+#ifndef STORE_DRAIN_MASK
+#define STORE_DRAIN_MASK 0xff
+#endif
+__device__ __forceinline__ void drain_stores(int stage) {
+  if ((STORE_DRAIN_MASK >> stage) & 1) wait_vmcnt<0>();
+}
+
 __device__ __forceinline__ void trace_ev(const KParams& P, int token, int stage, int what) {
   if (P.trace && token == P.trace_token && __lane_id() == 0)
     P.trace[((long)blockIdx.x * trace_stages(P.num_layers) + stage) * TRACE_EVENTS + what] = wall_clock64();
@@ -552,9 +562,6 @@ __device__ __forceinline__ float row2k(Shared* S, u32 n, int lane, const float (
 __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u32 epoch, int token) {
   Shared* S = W.C.S;
   const int lane = W.lane, par = l & 1, p = W.par_in;
-  const LDGLayerWeight& lw = S->lw[l];
-  const h8 w0 = *(const h8*)((const _Float16*)lw.input_layernorm_weight + 8 * lane);
-  const h8 w1 = *(const h8*)((const _Float16*)lw.input_layernorm_weight + 512 + 8 * lane);
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_POLL);
   float ss;
   if (l == 0) {
@@ -569,15 +576,16 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   if (lane == 0) S->red[p][W.c] = ss;
   sync4(W);
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_SYNC);
-  float a[8], b[8];
-  norm_act(S->vin[p], rstd_of(S->red[p]), w0, w1, a, b, lane);
-  const u32 n0 = W.gl;
+  const u32 n0 = W.gl;  // lines n0, n0 + 1: input norm weights; then the rows
   W.gl += LINES_QKV;
   wait_lines(W, W.gl);
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
+  float a[8], b[8];
+  norm_act(S->vin[p], rstd_of(S->red[p]), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
+           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b, lane);
   float part[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + 2 * (4 * W.c + r), lane, a, b);
+  for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + LINES_NORM + 2 * (4 * W.c + r), lane, a, b);
   release_lines(W, W.gl);
   // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
   const float rs = reduce4(part[0], part[1], part[2], part[3]);
@@ -585,6 +593,7 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   if (lane < 2)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_QKV) + (QKV_PER_WG / 2) * W.i + 2 * W.c + lane,
              lane == 0 ? pack_h2(r0, r1) : pack_h2(r2, r3), tag_of(epoch, l, S_QKV));
+  drain_stores(S_QKV);
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_STORE);
   W.par_in ^= 1;
 }
@@ -593,13 +602,8 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
 __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
   const int lane = W.lane, par = l & 1, p = W.par_in;
-  const LDGLayerWeight& lw = S->lw[l];
   const int pos = P.start_pos + t, ctx = pos + 1;
   const int d4 = 4 * (lane & 31);
-  const h4 cv = *(const h4*)(P.cos_t + (long)pos * HD + d4);
-  const h4 sv = *(const h4*)(P.sin_t + (long)pos * HD + d4);
-  const h4 qn = *(const h4*)((const _Float16*)lw.q_norm_weight + d4);
-  const h4 kn = *(const h4*)((const _Float16*)lw.k_norm_weight + d4);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_POLL);
   {  // quarter c: slots [64 c, 64 c + 64) of the group's 256 q|k|v slots
     const int voff[1] = {16 * lane};
@@ -612,8 +616,20 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
   sync4(W);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_SYNC);
+  // ring: line n0 = q_norm | k_norm | cos[pos] | sin[pos]; K lines n0 + 1 + m; V lines n0 + 1 + nk + m
+  const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
+  const u32 n0 = W.gl;
+  W.gl += LINES_ATTMISC + 2 * nk;
+  wait_lines(W, W.gl);
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
+  const u32 nkl = n0 + LINES_ATTMISC;  // first K line
   // every wave computes the same normed, roped q0 | q1 | k and v (identical writes to qr)
   {
+    const char* misc = (const char*)ring_line(S, n0);
+    const h4 qn = *(const h4*)(misc + 2 * d4);
+    const h4 kn = *(const h4*)(misc + 256 + 2 * d4);
+    const h4 cv = *(const h4*)(misc + 512 + 2 * d4);
+    const h4 sv = *(const h4*)(misc + 768 + 2 * d4);
     const float4 qv = *(const float4*)(S->vin[p] + 4 * lane);        // q head (lane / 32), dims d4
     const float4 kv = *(const float4*)(S->vin[p] + 256 + 4 * lane);  // k (lane < 32) or v, dims d4
     const float q[4] = {qv.x, qv.y, qv.z, qv.w};
@@ -654,9 +670,6 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     }
   }
   // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..
-  const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
-  const u32 n0 = W.gl;
-  W.gl += 2 * nk;
   const int j = lane >> 4, q16 = lane & 15;
   float qa[8], qb[8];
   {
@@ -665,8 +678,6 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     qa[0] = a0.x; qa[1] = a0.y; qa[2] = a0.z; qa[3] = a0.w; qa[4] = a1.x; qa[5] = a1.y; qa[6] = a1.z; qa[7] = a1.w;
     qb[0] = b0.x; qb[1] = b0.y; qb[2] = b0.z; qb[3] = b0.w; qb[4] = b1.x; qb[5] = b1.y; qb[6] = b1.z; qb[7] = b1.w;
   }
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
   // the current position is not in the cache lines (the loader reads a spare row for it):
   // the wave whose 16 positions include it writes its fp16 k and v into its own ring lines
   {
@@ -678,8 +689,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
                      (_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
       const h8 vh = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
                      (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
-      S->ring[(n0 + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, kh);
-      S->ring[(n0 + nk + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, vh);
+      S->ring[(nkl + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, kh);
+      S->ring[(nkl + nk + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, vh);
     }
   }
   float sc[4][2];
@@ -690,7 +701,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     valid[bb] = m < nk && t0 + 4 * m + j < t1;
     float s0 = 0.f, s1 = 0.f;
     if (m < nk) {
-      const v4u kw = ring_line(S, n0 + m)[lane];
+      const v4u kw = ring_line(S, nkl + m)[lane];
       s0 = dot8(kw, qa);
       s1 = dot8(kw, qb);
     }
@@ -719,7 +730,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   for (int bb = 0; bb < 4; ++bb) {
     const int m = 4 * W.c + bb;
     if (m < nk) {
-      const h8 vh = __builtin_bit_cast(h8, ring_line(S, n0 + nk + m)[lane]);
+      const h8 vh = __builtin_bit_cast(h8, ring_line(S, nkl + nk + m)[lane]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         acc[0][e] = fmaf(pr[0][bb], (float)vh[e], acc[0][e]);
@@ -778,6 +789,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       ll_store_xcd(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
     }
   }
+  drain_stores(S_ATT);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
   W.par_in ^= 1;
 }
@@ -817,6 +829,7 @@ __device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u
   const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
   if (lane < 4)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + lane, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
+  drain_stores(S_COMB);
   trace_ev(P, t, NSTAGE * l + S_COMB, TR_STORE);
 }
 
@@ -858,6 +871,7 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
     ll_store(P.ws, base + r, __float_as_uint(y0), tag_of(epoch, l, S_O));
     ll_store(P.ws, base + r + 4, __float_as_uint(y1), tag_of(epoch, l, S_O));
   }
+  drain_stores(S_O);
   trace_ev(P, t, NSTAGE * l + S_O, TR_STORE);
   W.par_in ^= 1;
 }
@@ -919,6 +933,7 @@ __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u3
       }
     }
   }
+  drain_stores(st);
   trace_ev(P, t, NSTAGE * l + st, TR_STORE);
   W.par_in ^= 1;
 }
@@ -927,9 +942,6 @@ __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u3
 __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
   const int lane = W.lane, par = l & 1, p = W.par_in;
-  const LDGLayerWeight& lw = S->lw[l];
-  const h8 w0 = *(const h8*)((const _Float16*)lw.post_attn_layernorm_weight + 8 * lane);
-  const h8 w1 = *(const h8*)((const _Float16*)lw.post_attn_layernorm_weight + 512 + 8 * lane);
   trace_ev(P, t, NSTAGE * l + S_GU, TR_POLL);
   float ss;
   if (P.mode == MODE_MLP) {
@@ -943,17 +955,19 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   if (lane == 0) S->red[p][W.c] = ss;
   sync4(W);
   trace_ev(P, t, NSTAGE * l + S_GU, TR_SYNC);
-  float a[8], b[8];
-  norm_act(S->vin[p], rstd_of(S->red[p]), w0, w1, a, b, lane);
-  const u32 n0 = W.gl;
+  const u32 n0 = W.gl;  // lines n0, n0 + 1: post-attention norm weights; then gate rows, up rows
   W.gl += LINES_GU;
   wait_lines(W, W.gl);
   trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
+  float a[8], b[8];
+  norm_act(S->vin[p], rstd_of(S->red[p]), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
+           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b, lane);
+  const u32 ng = n0 + LINES_NORM;
   float part[6];
 #pragma unroll
   for (int jj = 0; jj < 3; ++jj) {
-    part[jj] = row2k(S, n0 + 2 * (3 * W.c + jj), lane, a, b);                          // gate
-    part[3 + jj] = row2k(S, n0 + 2 * GU_PER_WG + 2 * (3 * W.c + jj), lane, a, b);      // up
+    part[jj] = row2k(S, ng + 2 * (3 * W.c + jj), lane, a, b);                          // gate
+    part[3 + jj] = row2k(S, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj), lane, a, b);      // up
   }
   release_lines(W, W.gl);
   float pq, qq;
@@ -966,6 +980,7 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   if (lane < 2)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_INT) + int_slot(W.i, W.c, lane), lane == 0 ? pack_h2(s0, s1) : pack_h2(s2, 0.f),
              tag_of(epoch, l, S_GU));
+  drain_stores(S_GU);
   trace_ev(P, t, NSTAGE * l + S_GU, TR_STORE);
   W.par_in ^= 1;
 }
@@ -1014,6 +1029,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
     ll_store(P.ws, base + r, __float_as_uint(y0), tag_of(epoch, l, S_DOWN));
     ll_store(P.ws, base + r + 4, __float_as_uint(y1), tag_of(epoch, l, S_DOWN));
   }
+  drain_stores(S_DOWN);
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_STORE);
   W.par_in ^= 1;
 }
@@ -1150,15 +1166,28 @@ struct Stream {
 __device__ __forceinline__ Stream make_stream(const KParams& P, const Shared* S, int si, int l, int x, int i, int pos,
                                               int ctx, int lane) {
   const LDGLayerWeight& lw = S->lw[l];
-  const StreamGeom g = stream_geom(si, x, i, ctx, pos, P.max_seq, lane);
-  const void* mats[9] = {lw.q_proj_weight, lw.k_proj_weight, lw.v_proj_weight,
-                         P.k_cache + ((long)l * NKV + x) * P.max_seq * HD, P.v_cache + ((long)l * NKV + x) * P.max_seq * HD,
-                         lw.o_proj_weight, lw.gate_proj_weight, lw.up_proj_weight, lw.down_proj_weight};
-  const _Float16* M = (const _Float16*)(g.mat == 0 ? mats[0] : g.mat == 1 ? mats[1] : g.mat == 2 ? mats[2]
-                                        : g.mat == 3 ? mats[3] : g.mat == 4 ? mats[4] : g.mat == 5 ? mats[5]
-                                        : g.mat == 6 ? mats[6] : g.mat == 7 ? mats[7] : mats[8]);
+  const StreamGeom g = stream_geom(si, x, i, ctx, pos, lane);
+  const long kv = ((long)l * NKV + x) * P.max_seq * HD;
+  const void* M;
+  switch (g.mat) {  // lane-uniform except for the attention-vector line
+    case 0: M = lw.q_proj_weight; break;
+    case 1: M = lw.k_proj_weight; break;
+    case 2: M = lw.v_proj_weight; break;
+    case 3: M = P.k_cache + kv; break;
+    case 4: M = P.v_cache + kv; break;
+    case 5: M = lw.o_proj_weight; break;
+    case 6: M = lw.gate_proj_weight; break;
+    case 7: M = lw.up_proj_weight; break;
+    case 8: M = lw.down_proj_weight; break;
+    case 9: M = lw.input_layernorm_weight; break;
+    case 10: M = lw.post_attn_layernorm_weight; break;
+    case 11: M = lw.q_norm_weight; break;
+    case 12: M = lw.k_norm_weight; break;
+    case 13: M = P.cos_t; break;
+    default: M = P.sin_t; break;
+  }
   Stream st;
-  st.base = (const char*)(M + g.elem0 + g.loff);
+  st.base = (const char*)((const _Float16*)M + g.elem0 + g.loff);
   st.stride = g.stride * 2;
   st.n = g.n;
   st.vlim = g.vlim;
@@ -1192,9 +1221,9 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
       u32 last = 0;     // last line issued
       int pending = 0;  // lines issued whose completion is not yet published
       const int nl = P.mode == MODE_MLP ? 1 : L;
-      const int s0 = P.mode == MODE_MLP ? 4 : 0;
+      const int s0 = P.mode == MODE_MLP ? MLP_FIRST_STREAM : 0;
       for (int l = 0; l < nl && C.ok; ++l) {
-        for (int si = s0; si < 7 && C.ok; ++si) {
+        for (int si = s0; si < NSTREAM && C.ok; ++si) {
           const Stream st = make_stream(P, S, si, l, x, i, pos, ctx, lane);
           const char* src = st.base;
           int m = (int)((u32)(q - (int)gl) & 3u);

@@ -85,9 +85,13 @@ QL_HD int att_nk(int ctx, int s) {  // K lines (= V lines) of split s
 // ---- LDS weight ring ---------------------------------------------------------------
 constexpr int RING_LINES = 128;
 constexpr int LINE_BYTES = 1024;
-constexpr int LINES_QKV = 32;   // 16 rows x 2 lines
+// The per-layer norm weights and the per-token RoPE row travel through the ring
+// too, so a compute wave never has a global load outstanding when it polls.
+constexpr int LINES_NORM = 2;   // a 1024-entry fp16 norm weight vector
+constexpr int LINES_QKV = LINES_NORM + 32;  // input norm, then 16 rows x 2 lines
+constexpr int LINES_ATTMISC = 1;  // q_norm | k_norm | cos[pos] | sin[pos], 256 B each
 constexpr int LINES_O = 16;     // 32 rows x 512 B, 2 rows per line
-constexpr int LINES_GU = 48;    // 12 gate rows then 12 up rows, 2 lines each
+constexpr int LINES_GU = LINES_NORM + 48;   // post-attention norm, then 12 gate rows, 12 up rows, 2 lines each
 constexpr int LINES_DOWN = 32;  // 32 rows x 768 B, one row per line (last 256 B unused)
 
 enum StageId : int { S_QKV = 0, S_ATT = 1, S_COMB = 2, S_O = 3, S_OSUM = 4, S_GU = 5, S_DOWN = 6, S_DSUM = 7 };
@@ -98,7 +102,7 @@ enum Mode : int { MODE_DECODE = 0, MODE_LMHEAD = 1, MODE_MLP = 2 };
 QL_HD int stage_lines(int st, int ctx, int s) {
   switch (st) {
     case S_QKV: return LINES_QKV;
-    case S_ATT: return 2 * att_nk(ctx, s);
+    case S_ATT: return LINES_ATTMISC + 2 * att_nk(ctx, s);
     case S_O: return LINES_O;
     case S_GU: return LINES_GU;
     case S_DOWN: return LINES_DOWN;
@@ -109,53 +113,71 @@ QL_HD int stage_lines(int st, int ctx, int s) {
 QL_HD int first_stage(int mode) { return mode == MODE_MLP ? S_GU : S_QKV; }
 
 // ---- loader streams ------------------------------------------------------------------
-// The ring lines of a layer come from 7 streams, in this order: 0 QKV (32 lines),
-// 1 K (nk), 2 V (nk), 3 o_proj (16), 4 gate (24), 5 up (24), 6 down (32). Line m
-// of a stream gives lane `lane` 8 fp16 values at element
+// The ring lines of a layer come from 10 streams, in this order: 0 input norm (2
+// lines), 1 QKV rows (32), 2 attention vectors (1), 3 K (nk), 4 V (nk), 5 o_proj
+// (16), 6 post-attention norm (2), 7 gate (24), 8 up (24), 9 down (32). Line m of
+// a stream gives lane `lane` 8 fp16 values at element
 //   elem0 + m * stride + loff
-// of the stream's matrix (mat: 0..2 = Wq/Wk/Wv, 3 K cache, 4 V cache, 5 Wo,
-// 6 Wg, 7 Wu, 8 Wd; cache elements counted from layer l's kv head x at position
-// 0). For K/V lines, lanes whose position index 4 m + lane / 16 is >= vlim
-// read no cache element (they read a fixed spare row instead).
-constexpr int NSTREAM = 7;
+// of the lane's source array `mat`: 0..2 Wq/Wk/Wv, 3 K cache, 4 V cache, 5 Wo,
+// 6 Wg, 7 Wu, 8 Wd, 9 input norm, 10 post-attention norm, 11 q_norm, 12 k_norm,
+// 13 cos table, 14 sin table (cache elements counted from layer l's kv head x at
+// position 0). Only the attention-vector line mixes sources: lanes 0-15 q_norm,
+// 16-31 k_norm, 32-47 cos[pos], 48-63 sin[pos]. For K/V lines, lanes whose
+// position index 4 m + lane / 16 is >= vlim read no cache element (they read a
+// fixed spare row instead).
+constexpr int NSTREAM = 10;
+constexpr int MLP_FIRST_STREAM = 6;
 struct StreamGeom {
   int mat;
   long elem0, stride, loff;
   int n, vlim;
 };
-QL_HD StreamGeom stream_geom(int si, int x, int i, int ctx, int pos, int max_seq, int lane) {
+QL_HD StreamGeom stream_geom(int si, int x, int i, int ctx, int pos, int lane) {
   StreamGeom g;
   g.vlim = 0x7fffffff;
   g.loff = 8 * lane;
   g.stride = 512;
   switch (si) {
-    case 0: {
+    case 0:
+    case 6:
+      g.mat = si == 0 ? 9 : 10;
+      g.elem0 = 0;
+      g.n = LINES_NORM;
+      break;
+    case 1: {
       const int gr = QKV_PER_WG * i;
       g.mat = grp_matrix(gr);
       g.elem0 = (long)grp_row_in(x, gr) * HIDDEN;
-      g.n = LINES_QKV;
+      g.n = LINES_QKV - LINES_NORM;
       break;
     }
-    case 1:
     case 2: {
-      const int t0 = att_t0(ctx, i), t1 = att_t1(ctx, i);
-      g.mat = si == 1 ? 3 : 4;
-      g.elem0 = (long)t0 * HD;
-      g.n = att_nk(ctx, i);
-      g.vlim = (t1 < pos ? t1 : pos) - t0;
-      (void)max_seq;
+      const int seg = lane >> 4;
+      g.mat = 11 + seg;
+      g.elem0 = seg >= 2 ? (long)pos * HD : 0;
+      g.loff = 8 * (lane & 15);
+      g.n = LINES_ATTMISC;
       break;
     }
     case 3:
+    case 4: {
+      const int t0 = att_t0(ctx, i), t1 = att_t1(ctx, i);
+      g.mat = si == 3 ? 3 : 4;
+      g.elem0 = (long)t0 * HD;
+      g.n = att_nk(ctx, i);
+      g.vlim = (t1 < pos ? t1 : pos) - t0;
+      break;
+    }
+    case 5:
       g.mat = 5;
       g.elem0 = (long)HROWS * i * QSZ + OCOLS * x;
       g.stride = 2L * QSZ;
       g.loff = (long)(lane >> 5) * QSZ + 8 * (lane & 31);
       g.n = LINES_O;
       break;
-    case 4:
-    case 5:
-      g.mat = si == 4 ? 6 : 7;
+    case 7:
+    case 8:
+      g.mat = si == 7 ? 6 : 7;
       g.elem0 = (long)(ICOLS * x + GU_PER_WG * i) * HIDDEN;
       g.n = 2 * GU_PER_WG;
       break;
