@@ -271,13 +271,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 struct Shared {
   v4u ring[RING_LINES][LINE_BYTES / 16];  // 128 KB weight / K-V line ring (must stay first: LDS offset 0)
-  float vin[2][HIDDEN];            // stage input (fp32), alternating between stages
-  float red[2][NCW];               // per-wave partial sums of squares, alternating
-  float qr[4 * HD];                // roped q (2 heads), roped k, v of the current position
+  float wbuf[NCW][4 * HD];          // per-wave scratch: roped q | k | v (attention), down-input reshuffle
   float apart[NCW][2][PART_PER_HEAD];  // per-wave attention partials (m, l, acc)
-  float opart[2][NXCD][HROWS];     // per-XCD partial rows for the residual sums, alternating
-  float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32)
-  float actres[HROWS];             // fp32 post-attention residual, same rows
+  float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32) (compute wave 0 only)
+  float actres[HROWS];             // fp32 post-attention residual, same rows (compute wave 0 only)
   float xfin[HIDDEN];              // lm_head input (fp32)
   float lmv[NCW + NLW];            // per-wave lm_head best value
   int lmi[NCW + NLW];              // per-wave lm_head best row
@@ -321,23 +318,32 @@ __device__ __forceinline__ bool give_up(Ctl& C, u64 t0, int& spins) {
 
 // Polls K slot pairs per lane until both slots of every pair carry `tag`. Pair k
 // of this lane is at byte voff[k] + soff of the workspace (soff wave-uniform).
-// Lanes with active == false take no part.
-template <int K>
-__device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int soff, bool active, v4u (&out)[K]) {
+// Lanes with active == false take no part. `first` runs once, after the first
+// sweep's loads are issued (the ring check of the stage hides behind their latency).
+struct NoPre {
+  __device__ void operator()() const {}
+};
+template <int K, typename Pre = NoPre>
+__device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int soff, bool active, v4u (&out)[K],
+                                     Pre first = Pre()) {
   bool done[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     done[k] = !active;
     out[k] = v4u{0, 0, 0, 0};
   }
-  if (!C.ok) return;
+  if (!C.ok) {
+    first();
+    return;
+  }
   const u64 t0 = wall_clock64();
   int spins = 0;
-  for (;;) {
+  for (bool once = true;; once = false) {
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < K; ++k)
       if (!done[k]) out[k] = ld_pair(C.r, voff[k], soff);
+    if (once) first();
     bool all = true;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -471,7 +477,6 @@ struct CW {
   Ctl C;
   int w, x, i, c, lane;
   u32 nsync;   // barriers passed
-  int par_in;  // vin / red / opart buffer parity of the current stage
   u32 gl;      // global ring line index of the next stage
 };
 
@@ -512,38 +517,50 @@ __device__ __forceinline__ void release_lines(CW& W, u32 end) {
   if (W.lane == 0) lds_st(&W.C.S->cons[W.c], end);
 }
 
-// polls a quarter (128 slots = 256 values) of a 1024-value H2 vector into vin;
-// returns the lane's sum of squares of its 4 values
-__device__ __forceinline__ float poll_quarter1024(CW& W, u32 tag, long base_slot, float* vin) {
+// Stage inputs go straight from the exchange slots into each compute wave's
+// registers: every wave polls the whole vector it needs, so no stage waits for the
+// workgroup's other waves before it computes.
+
+// slots (2 s, 2 s + 1) of a b128 pair -> values 4 s .. 4 s + 3 of an H2 vector
+__device__ __forceinline__ void unpack8(v4u p, v4u q, float (&x)[8]) {
+  x[0] = lo_h(p.x); x[1] = hi_h(p.x); x[2] = lo_h(p.z); x[3] = hi_h(p.z);
+  x[4] = lo_h(q.x); x[5] = hi_h(q.x); x[6] = lo_h(q.z); x[7] = hi_h(q.z);
+}
+__device__ __forceinline__ float sumsq16(const float (&xa)[8], const float (&xb)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s = fmaf(xa[e], xa[e], fmaf(xb[e], xb[e], s));
+  return s;
+}
+// the lane's values x[8 lane, +8) and x[512 + 8 lane, +8) of a 1024-value H2 vector in
+// slots [base_slot, base_slot + 512); returns their sum of squares
+template <typename Pre>
+__device__ __forceinline__ float poll_x1024(CW& W, u32 tag, long base_slot, float (&xa)[8], float (&xb)[8], Pre first) {
   const int lane = W.lane;
-  const int voff[1] = {16 * lane};
-  v4u v[1];
-  poll<1>(W.C, tag, voff, (int)((base_slot + 128 * W.c) * 8), true, v);
-  const float a = lo_h(v[0].x), b = hi_h(v[0].x), cc = lo_h(v[0].z), d = hi_h(v[0].z);
-  *(float4*)(vin + 256 * W.c + 4 * lane) = make_float4(a, b, cc, d);
-  return a * a + b * b + cc * cc + d * d;
+  const int voff[4] = {32 * lane, 32 * lane + 16, 2048 + 32 * lane, 2048 + 32 * lane + 16};
+  v4u v[4];
+  poll<4>(W.C, tag, voff, (int)(base_slot * 8), true, v, first);
+  unpack8(v[0], v[1], xa);
+  unpack8(v[2], v[3], xb);
+  return sumsq16(xa, xb);
 }
-
-// loads a quarter of a 1024-value fp16 vector from global memory into vin (embedding row / MLP input)
-__device__ __forceinline__ float load_quarter1024(CW& W, const _Float16* src, float* vin) {
-  const h4 v = *(const h4*)(src + 256 * W.c + 4 * W.lane);
-  const float a = (float)v[0], b = (float)v[1], cc = (float)v[2], d = (float)v[3];
-  *(float4*)(vin + 256 * W.c + 4 * W.lane) = make_float4(a, b, cc, d);
-  return a * a + b * b + cc * cc + d * d;
+// the same from a 1024-value fp16 vector in global memory (embedding row, MLP input)
+__device__ __forceinline__ float load_x1024(const _Float16* src, int lane, float (&xa)[8], float (&xb)[8]) {
+  const h8 p = *(const h8*)(src + 8 * lane), q = *(const h8*)(src + 512 + 8 * lane);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xa[e] = (float)p[e];
+    xb[e] = (float)q[e];
+  }
+  return sumsq16(xa, xb);
 }
-
-__device__ __forceinline__ float rstd_of(const float* red) {
-  const float ss = (red[0] + red[1]) + (red[2] + red[3]);
-  return rsqrtf(ss * (1.0f / HIDDEN) + RMS_EPS);
+__device__ __forceinline__ float rstd_of(float lane_ss) {
+  return rsqrtf(wave_sum(lane_ss) * (1.0f / HIDDEN) + RMS_EPS);
 }
 
 // the lane's 16 normalised activations a = x[8 l .. 8 l + 8), b = x[512 + 8 l ..]
-__device__ __forceinline__ void norm_act(const float* vin, float rstd, const h8& w0, const h8& w1, float (&a)[8],
-                                         float (&b)[8], int lane) {
-  const float4 p0 = *(const float4*)(vin + 8 * lane), p1 = *(const float4*)(vin + 8 * lane + 4);
-  const float4 q0 = *(const float4*)(vin + 512 + 8 * lane), q1 = *(const float4*)(vin + 512 + 8 * lane + 4);
-  const float xa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-  const float xb[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+__device__ __forceinline__ void norm_act(const float (&xa)[8], const float (&xb)[8], float rstd, const h8& w0,
+                                         const h8& w1, float (&a)[8], float (&b)[8]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     a[e] = xa[e] * rstd * (float)w0[e];
@@ -561,28 +578,23 @@ __device__ __forceinline__ float row2k(Shared* S, u32 n, int lane, const float (
 // QKV: rows [16 i + 4 c, +4) of the kv group from the normalised residual
 __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u32 epoch, int token) {
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_POLL);
-  float ss;
-  if (l == 0) {
-    const _Float16* row = P.embed + (long)token * HIDDEN;
-    ss = load_quarter1024(W, row, S->vin[p]);
-    if (W.c == 0 && lane < HROWS) S->resid[lane] = (float)row[HROWS * W.i + lane];
-  } else {
-    ss = poll_quarter1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), S->vin[p]);
-  }
-  trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
-  ss = wave_sum(ss);
-  if (lane == 0) S->red[p][W.c] = ss;
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + S_QKV, TR_SYNC);
   const u32 n0 = W.gl;  // lines n0, n0 + 1: input norm weights; then the rows
   W.gl += LINES_QKV;
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
+  float xa[8], xb[8], ss;
+  if (l == 0) {
+    const _Float16* row = P.embed + (long)token * HIDDEN;
+    ss = load_x1024(row, lane, xa, xb);
+    if (W.c == 0 && lane < HROWS) S->resid[lane] = (float)row[HROWS * W.i + lane];
+    wait_lines(W, W.gl);
+  } else {
+    ss = poll_x1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), xa, xb, [&] { wait_lines(W, W.gl); });
+  }
+  trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
   float a[8], b[8];
-  norm_act(S->vin[p], rstd_of(S->red[p]), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
-           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b, lane);
+  norm_act(xa, xb, rstd_of(ss), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
+           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b);
   float part[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + LINES_NORM + 2 * (4 * W.c + r), lane, a, b);
@@ -595,43 +607,39 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
              lane == 0 ? pack_h2(r0, r1) : pack_h2(r2, r3), tag_of(epoch, l, S_QKV));
   drain_stores(S_QKV);
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_STORE);
-  W.par_in ^= 1;
 }
 
 // attention split i of kv head x: q/k norms, RoPE, K/V write, 16 positions per wave, merge
 __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   const int pos = P.start_pos + t, ctx = pos + 1;
   const int d4 = 4 * (lane & 31);
+  float* qr = S->wbuf[W.c];
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_POLL);
-  {  // quarter c: slots [64 c, 64 c + 64) of the group's 256 q|k|v slots
-    const int voff[1] = {16 * lane};
-    v4u v[1];
-    poll<1>(W.C, tag_of(epoch, l, S_QKV), voff, (int)((xbuf(par, W.x, B_QKV) + 64 * W.c) * 8), lane < 32, v);
-    if (lane < 32)
-      *(float4*)(S->vin[p] + 128 * W.c + 4 * lane) =
-          make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
-  }
-  trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + S_ATT, TR_SYNC);
   // ring: line n0 = q_norm | k_norm | cos[pos] | sin[pos]; K lines n0 + 1 + m; V lines n0 + 1 + nk + m
   const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
   const u32 n0 = W.gl;
   W.gl += LINES_ATTMISC + 2 * nk;
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
+  // the group's 512 q0 | q1 | k | v values: this lane's q values [4 lane, +4) and k | v values [256 + 4 lane, +4)
+  float4 qv, kv;
+  {
+    const int voff[2] = {16 * lane, 1024 + 16 * lane};
+    v4u v[2];
+    poll<2>(W.C, tag_of(epoch, l, S_QKV), voff, (int)(xbuf(par, W.x, B_QKV) * 8), true, v,
+            [&] { wait_lines(W, W.gl); });
+    qv = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
+    kv = make_float4(lo_h(v[1].x), hi_h(v[1].x), lo_h(v[1].z), hi_h(v[1].z));
+  }
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
   const u32 nkl = n0 + LINES_ATTMISC;  // first K line
-  // every wave computes the same normed, roped q0 | q1 | k and v (identical writes to qr)
+  // every wave computes the normed, roped q0 | q1 | k and v into its own scratch
   {
     const char* misc = (const char*)ring_line(S, n0);
     const h4 qn = *(const h4*)(misc + 2 * d4);
     const h4 kn = *(const h4*)(misc + 256 + 2 * d4);
     const h4 cv = *(const h4*)(misc + 512 + 2 * d4);
     const h4 sv = *(const h4*)(misc + 768 + 2 * d4);
-    const float4 qv = *(const float4*)(S->vin[p] + 4 * lane);        // q head (lane / 32), dims d4
-    const float4 kv = *(const float4*)(S->vin[p] + 256 + 4 * lane);  // k (lane < 32) or v, dims d4
     const float q[4] = {qv.x, qv.y, qv.z, qv.w};
     const float k[4] = {kv.x, kv.y, kv.z, kv.w};
     const float rq = rsqrtf(half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]) * (1.0f / HD) + RMS_EPS);
@@ -652,11 +660,11 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       qo[j] = qq[j] * cs + qp * sn;
       ko[j] = kk[j] * cs + kp * sn;
     }
-    *(float4*)(S->qr + 4 * lane) = make_float4(qo[0], qo[1], qo[2], qo[3]);
+    *(float4*)(qr + 4 * lane) = make_float4(qo[0], qo[1], qo[2], qo[3]);
     if (lane < 32)
-      *(float4*)(S->qr + 256 + 4 * lane) = make_float4(ko[0], ko[1], ko[2], ko[3]);
+      *(float4*)(qr + 256 + 4 * lane) = make_float4(ko[0], ko[1], ko[2], ko[3]);
     else
-      *(float4*)(S->qr + 256 + 4 * lane) = make_float4(k[0], k[1], k[2], k[3]);
+      *(float4*)(qr + 256 + 4 * lane) = make_float4(k[0], k[1], k[2], k[3]);
     // the split holding `pos` writes this position's K (roped) and V to the cache
     if (W.c == 0 && att_t0(ctx, W.i) <= pos && pos < att_t1(ctx, W.i)) {
       const long row = (((long)l * NKV + W.x) * P.max_seq + pos) * HD + d4;
@@ -673,8 +681,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   const int j = lane >> 4, q16 = lane & 15;
   float qa[8], qb[8];
   {
-    const float4 a0 = *(const float4*)(S->qr + 8 * q16), a1 = *(const float4*)(S->qr + 8 * q16 + 4);
-    const float4 b0 = *(const float4*)(S->qr + 128 + 8 * q16), b1 = *(const float4*)(S->qr + 128 + 8 * q16 + 4);
+    const float4 a0 = *(const float4*)(qr + 8 * q16), a1 = *(const float4*)(qr + 8 * q16 + 4);
+    const float4 b0 = *(const float4*)(qr + 128 + 8 * q16), b1 = *(const float4*)(qr + 128 + 8 * q16 + 4);
     qa[0] = a0.x; qa[1] = a0.y; qa[2] = a0.z; qa[3] = a0.w; qa[4] = a1.x; qa[5] = a1.y; qa[6] = a1.z; qa[7] = a1.w;
     qb[0] = b0.x; qb[1] = b0.y; qb[2] = b0.z; qb[3] = b0.w; qb[4] = b1.x; qb[5] = b1.y; qb[6] = b1.z; qb[7] = b1.w;
   }
@@ -683,8 +691,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   {
     const int mp = (pos - t0) >> 2, jp = (pos - t0) & 3;
     if (pos >= t0 && pos < t1 && (mp >> 2) == W.c && j == jp) {
-      const float4 k0 = *(const float4*)(S->qr + 256 + 8 * q16), k1 = *(const float4*)(S->qr + 256 + 8 * q16 + 4);
-      const float4 v0 = *(const float4*)(S->qr + 384 + 8 * q16), v1 = *(const float4*)(S->qr + 384 + 8 * q16 + 4);
+      const float4 k0 = *(const float4*)(qr + 256 + 8 * q16), k1 = *(const float4*)(qr + 256 + 8 * q16 + 4);
+      const float4 v0 = *(const float4*)(qr + 384 + 8 * q16), v1 = *(const float4*)(qr + 384 + 8 * q16 + 4);
       const h8 kh = {(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w,
                      (_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
       const h8 vh = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
@@ -791,7 +799,6 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   }
   drain_stores(S_ATT);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
-  W.par_in ^= 1;
 }
 
 // combine (wave 0): q head 2x + i / 16, dims [8 (i % 16), +8) over the 32 splits
@@ -836,28 +843,19 @@ __device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u
 // o_proj partial of the XCD: rows [32 i + 8 c, +8) over the XCD's 256 attention dims
 __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   trace_ev(P, t, NSTAGE * l + S_O, TR_POLL);
-  {  // quarter c: slots [32 c, 32 c + 32) = values [64 c, 64 c + 64)
-    const int voff[1] = {16 * lane};
-    v4u v[1];
-    poll<1>(W.C, tag_of(epoch, l, S_COMB), voff, (int)((xbuf(par, W.x, B_ATTO) + 32 * W.c) * 8), lane < 16, v);
-    if (lane < 16)
-      *(float4*)(S->vin[p] + 64 * W.c + 4 * lane) =
-          make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
-  }
-  trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + S_O, TR_SYNC);
-  float a[8];
-  {
-    const float4 a0 = *(const float4*)(S->vin[p] + 8 * (lane & 31)), a1 = *(const float4*)(S->vin[p] + 8 * (lane & 31) + 4);
-    a[0] = a0.x; a[1] = a0.y; a[2] = a0.z; a[3] = a0.w; a[4] = a1.x; a[5] = a1.y; a[6] = a1.z; a[7] = a1.w;
-  }
   const u32 n0 = W.gl;
   W.gl += LINES_O;
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
+  float a[8];  // attention output values [8 (lane % 32), +8)
+  {
+    const int voff[2] = {32 * (lane & 31), 32 * (lane & 31) + 16};
+    v4u v[2];
+    poll<2>(W.C, tag_of(epoch, l, S_COMB), voff, (int)(xbuf(par, W.x, B_ATTO) * 8), true, v,
+            [&] { wait_lines(W, W.gl); });
+    unpack8(v[0], v[1], a);
+  }
+  trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
   // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
   float part[4];
 #pragma unroll
@@ -873,95 +871,80 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   }
   drain_stores(S_O);
   trace_ev(P, t, NSTAGE * l + S_O, TR_STORE);
-  W.par_in ^= 1;
 }
 
-// sum of the 8 per-XCD partials of rows [32 i, 32 i + 32) plus the residual;
-// `src` is B_OP (o_proj, producing the post-attention residual) or B_DP (down,
-// producing the next layer's residual)
+// sum of the 8 per-XCD partials of rows [32 i, 32 i + 32) plus the residual, by
+// compute wave 0 alone (the other waves go on to the next stage's poll); `src` is
+// B_OP (o_proj, producing the post-attention residual) or B_DP (down, producing the
+// next layer's residual)
 __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u32 epoch, bool is_down) {
+  if (W.c != 0) return;
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   const int st = is_down ? S_DSUM : S_OSUM;
+  const int q = lane & 7;  // rows 4 q .. 4 q + 3
   trace_ev(P, t, NSTAGE * l + st, TR_POLL);
-  {  // XCDs 2c, 2c + 1: lane < 32 reads XCD 2c + lane / 16, rows 2 (lane % 16), +1
-    const int g = 2 * W.c + ((lane >> 4) & 1);
-    const long src0 = xbuf(par, 2 * W.c, is_down ? B_DP : B_OP) + HROWS * W.i;
-    const int voff[1] = {(int)(((long)((lane >> 4) & 1) * XCD_SLOTS + 2 * (lane & 15)) * 8)};
-    v4u v[1];
-    poll<1>(W.C, tag_of(epoch, l, is_down ? S_DOWN : S_O), voff, (int)(src0 * 8), lane < 32, v);
-    if (lane < 32) {
-      S->opart[p][g][2 * (lane & 15)] = __uint_as_float(v[0].x);
-      S->opart[p][g][2 * (lane & 15) + 1] = __uint_as_float(v[0].z);
-    }
+  float y[4];
+  {  // lane: XCD lane / 8, rows 4 q .. 4 q + 3
+    const long src0 = xbuf(par, 0, is_down ? B_DP : B_OP) + HROWS * W.i;
+    const int off = (int)(((long)(lane >> 3) * XCD_SLOTS + 4 * q) * 8);
+    const int voff[2] = {off, off + 16};
+    v4u v[2];
+    poll<2>(W.C, tag_of(epoch, l, is_down ? S_DOWN : S_O), voff, (int)(src0 * 8), true, v);
+    y[0] = __uint_as_float(v[0].x);
+    y[1] = __uint_as_float(v[0].z);
+    y[2] = __uint_as_float(v[1].x);
+    y[3] = __uint_as_float(v[1].z);
   }
   trace_ev(P, t, NSTAGE * l + st, TR_INPUT);
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + st, TR_SYNC);
-  if (lane < 4) {  // rows 8c + 2 lane, +1
-    const int r = 8 * W.c + 2 * lane;
-    float s0 = is_down ? S->actres[r] : S->resid[r];
-    float s1 = is_down ? S->actres[r + 1] : S->resid[r + 1];
 #pragma unroll
-    for (int g = 0; g < NXCD; ++g) {
-      s0 += S->opart[p][g][r];
-      s1 += S->opart[p][g][r + 1];
-    }
-    if (is_down) {
-      S->resid[r] = s0;
-      S->resid[r + 1] = s1;
-    } else {
-      S->actres[r] = s0;
-      S->actres[r + 1] = s1;
-    }
+  for (int e = 0; e < 4; ++e) {  // over the 8 XCDs: lanes q, q + 8, ..., q + 56
+    y[e] += dpp<ROR8>(y[e]);
+    y[e] = rows4_sum(y[e]);
+  }
+  if (lane < 8) {
+    float* res = is_down ? S->actres : S->resid;  // input residual
+    float* out = is_down ? S->resid : S->actres;
+    const float4 r = *(const float4*)(res + 4 * q);
+    const float s0 = y[0] + r.x, s1 = y[1] + r.y, s2 = y[2] + r.z, s3 = y[3] + r.w;
+    *(float4*)(out + 4 * q) = make_float4(s0, s1, s2, s3);
+    const int row = HROWS * W.i + 4 * q;
     if (P.mode == MODE_MLP) {
-      if (W.x == 0) {
-        P.out_vec[HROWS * W.i + r] = s0;
-        P.out_vec[HROWS * W.i + r + 1] = s1;
-      }
+      if (W.x == 0) *(float4*)(P.out_vec + row) = make_float4(s0, s1, s2, s3);
     } else {
-      ll_store_xcd(P.ws, xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 4 * W.c + lane, pack_h2(s0, s1),
-               tag_of(epoch, l, st));
+      const long slot = xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 2 * q;
+      ll_store_xcd(P.ws, slot, pack_h2(s0, s1), tag_of(epoch, l, st));
+      ll_store_xcd(P.ws, slot + 1, pack_h2(s2, s3), tag_of(epoch, l, st));
       if (is_down && l == P.num_layers - 1 && W.x == 0) {  // final-layer residual
-        const int row = HROWS * W.i + r;
-        if (P.hidden_steps) {
-          P.hidden_steps[(long)t * HIDDEN + row] = s0;
-          P.hidden_steps[(long)t * HIDDEN + row + 1] = s1;
-        }
-        P.hidden_out[row] = (_Float16)s0;
-        P.hidden_out[row + 1] = (_Float16)s1;
+        if (P.hidden_steps) *(float4*)(P.hidden_steps + (long)t * HIDDEN + row) = make_float4(s0, s1, s2, s3);
+        const h4 ho = {(_Float16)s0, (_Float16)s1, (_Float16)s2, (_Float16)s3};
+        *(h4*)(P.hidden_out + row) = ho;
       }
     }
   }
   drain_stores(st);
   trace_ev(P, t, NSTAGE * l + st, TR_STORE);
-  W.par_in ^= 1;
 }
 
 // gate/up rows 384 x + 12 i + 3 c + {0, 1, 2} -> SiLU(gate) * up
 __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   trace_ev(P, t, NSTAGE * l + S_GU, TR_POLL);
-  float ss;
-  if (P.mode == MODE_MLP) {
-    ss = load_quarter1024(W, P.in_vec, S->vin[p]);
-    if (W.c == 0 && lane < HROWS) S->actres[lane] = (float)P.in_vec[HROWS * W.i + lane];
-  } else {
-    ss = poll_quarter1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), S->vin[p]);
-  }
-  trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
-  ss = wave_sum(ss);
-  if (lane == 0) S->red[p][W.c] = ss;
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + S_GU, TR_SYNC);
   const u32 n0 = W.gl;  // lines n0, n0 + 1: post-attention norm weights; then gate rows, up rows
   W.gl += LINES_GU;
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
+  float xa[8], xb[8], ss;
+  if (P.mode == MODE_MLP) {
+    ss = load_x1024(P.in_vec, lane, xa, xb);
+    if (W.c == 0 && lane < HROWS) S->actres[lane] = (float)P.in_vec[HROWS * W.i + lane];
+    wait_lines(W, W.gl);
+  } else {
+    ss = poll_x1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), xa, xb, [&] { wait_lines(W, W.gl); });
+  }
+  trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
   float a[8], b[8];
-  norm_act(S->vin[p], rstd_of(S->red[p]), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
-           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b, lane);
+  norm_act(xa, xb, rstd_of(ss), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
+           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b);
   const u32 ng = n0 + LINES_NORM;
   float part[6];
 #pragma unroll
@@ -982,41 +965,35 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
              tag_of(epoch, l, S_GU));
   drain_stores(S_GU);
   trace_ev(P, t, NSTAGE * l + S_GU, TR_STORE);
-  W.par_in ^= 1;
 }
 
 // down partial of the XCD: rows [32 i + 8 c, +8) over the XCD's 384 inter values
 __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u32 epoch) {
   Shared* S = W.C.S;
-  const int lane = W.lane, par = l & 1, p = W.par_in;
+  const int lane = W.lane, par = l & 1;
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_POLL);
-  {  // quarter c: slots [64 c, 64 c + 64): pair k = 32 c + lane = workgroup k / 4, wave k % 4
-    const int voff[1] = {16 * lane};
-    v4u v[1];
-    poll<1>(W.C, tag_of(epoch, l, S_GU), voff, (int)((xbuf(par, W.x, B_INT) + 64 * W.c) * 8), lane < 32, v);
-    if (lane < 32) {
-      const int k = 32 * W.c + lane;
-      float* dst = S->vin[p] + GU_PER_WG * (k >> 2) + 3 * (k & 3);
-      dst[0] = lo_h(v[0].x);
-      dst[1] = hi_h(v[0].x);
-      dst[2] = lo_h(v[0].z);
-    }
-  }
-  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
-  sync4(W);
-  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_SYNC);
+  const u32 n0 = W.gl;
+  W.gl += LINES_DOWN;
   float a[8];
-  {  // lanes 0-47 own inter values [8 l, 8 l + 8); lanes 48-63 contribute nothing
+  {
+    // slots [4 lane, 4 lane + 4) = workgroup lane / 2, waves 2 (lane % 2), +1: inter values
+    // [6 lane, 6 lane + 6) (each wave's second slot carries one value and padding);
+    // reshuffled through the wave's scratch so lanes 0-47 hold [8 lane, 8 lane + 8)
+    const int voff[2] = {32 * lane, 32 * lane + 16};
+    v4u v[2];
+    poll<2>(W.C, tag_of(epoch, l, S_GU), voff, (int)(xbuf(par, W.x, B_INT) * 8), true, v,
+            [&] { wait_lines(W, W.gl); });
+    float* d = S->wbuf[W.c];
+    *(float2*)(d + 6 * lane) = make_float2(lo_h(v[0].x), hi_h(v[0].x));
+    *(float2*)(d + 6 * lane + 2) = make_float2(lo_h(v[0].z), lo_h(v[1].x));
+    *(float2*)(d + 6 * lane + 4) = make_float2(hi_h(v[1].x), lo_h(v[1].z));
     const int o = lane < 48 ? 8 * lane : 0;
-    const float4 a0 = *(const float4*)(S->vin[p] + o), a1 = *(const float4*)(S->vin[p] + o + 4);
-    const float z = lane < 48 ? 1.f : 0.f;
+    const float4 a0 = *(const float4*)(d + o), a1 = *(const float4*)(d + o + 4);
+    const float z = lane < 48 ? 1.f : 0.f;  // lanes 48-63 contribute nothing
     a[0] = a0.x * z; a[1] = a0.y * z; a[2] = a0.z * z; a[3] = a0.w * z;
     a[4] = a1.x * z; a[5] = a1.y * z; a[6] = a1.z * z; a[7] = a1.w * z;
   }
-  const u32 n0 = W.gl;
-  W.gl += LINES_DOWN;
-  wait_lines(W, W.gl);
-  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
+  trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
   float part[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) part[r] = dot8(ring_line(S, n0 + 8 * W.c + r)[lane], a);
@@ -1031,33 +1008,34 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   }
   drain_stores(S_DOWN);
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_STORE);
-  W.par_in ^= 1;
 }
 
 // lm_head input: final RMSNorm of the all-gathered residual (decode) or the caller's vector
 __device__ __forceinline__ void st_lm_input(CW& W, const KParams& P, int t, u32 epoch) {
   Shared* S = W.C.S;
-  const int lane = W.lane, p = W.par_in, L = P.num_layers;
-  const int o = 256 * W.c + 4 * lane;
+  const int lane = W.lane, L = P.num_layers;
   if (P.mode == MODE_LMHEAD) {
+    const int o = 256 * W.c + 4 * lane;
     const h4 v = *(const h4*)(P.in_vec + o);
     *(float4*)(S->xfin + o) = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
   } else {
-    const h4 wf = *(const h4*)(P.final_norm + o);
+    // every wave normalises the whole vector and stores it (identical values)
+    const h8 w0 = *(const h8*)(P.final_norm + 8 * lane), w1 = *(const h8*)(P.final_norm + 512 + 8 * lane);
     trace_ev(P, t, NSTAGE * L, TR_POLL);
-    float ss = poll_quarter1024(W, tag_of(epoch, L - 1, S_DSUM), xbuf((L - 1) & 1, W.x, B_X), S->vin[p]);
+    float xa[8], xb[8], a[8], b[8];
+    const float ss = poll_x1024(W, tag_of(epoch, L - 1, S_DSUM), xbuf((L - 1) & 1, W.x, B_X), xa, xb, NoPre());
     trace_ev(P, t, NSTAGE * L, TR_INPUT);
-    ss = wave_sum(ss);
-    if (lane == 0) S->red[p][W.c] = ss;
-    sync4(W);
-    trace_ev(P, t, NSTAGE * L, TR_SYNC);
-    const float rs = rstd_of(S->red[p]);
-    const float4 xv = *(const float4*)(S->vin[p] + o);
-    const float4 nv = make_float4(xv.x * rs * (float)wf[0], xv.y * rs * (float)wf[1], xv.z * rs * (float)wf[2],
-                                  xv.w * rs * (float)wf[3]);
-    *(float4*)(S->xfin + o) = nv;
-    if (W.w == 0) *(float4*)(P.norm_out + o) = nv;
-    W.par_in ^= 1;
+    norm_act(xa, xb, rstd_of(ss), w0, w1, a, b);
+    *(float4*)(S->xfin + 8 * lane) = make_float4(a[0], a[1], a[2], a[3]);
+    *(float4*)(S->xfin + 8 * lane + 4) = make_float4(a[4], a[5], a[6], a[7]);
+    *(float4*)(S->xfin + 512 + 8 * lane) = make_float4(b[0], b[1], b[2], b[3]);
+    *(float4*)(S->xfin + 512 + 8 * lane + 4) = make_float4(b[4], b[5], b[6], b[7]);
+    if (W.w == 0 && W.c == 0) {
+      *(float4*)(P.norm_out + 8 * lane) = make_float4(a[0], a[1], a[2], a[3]);
+      *(float4*)(P.norm_out + 8 * lane + 4) = make_float4(a[4], a[5], a[6], a[7]);
+      *(float4*)(P.norm_out + 512 + 8 * lane) = make_float4(b[0], b[1], b[2], b[3]);
+      *(float4*)(P.norm_out + 512 + 8 * lane + 4) = make_float4(b[4], b[5], b[6], b[7]);
+    }
   }
   lds_release();
   if (lane == 0) __hip_atomic_fetch_add(&S->xfin_cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1076,7 +1054,6 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
   W.c = c;
   W.lane = __lane_id();
   W.nsync = 0;
-  W.par_in = 0;
   W.gl = 0;
   const int L = P.num_layers;
   int token = P.first_token;
