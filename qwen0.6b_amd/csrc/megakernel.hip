@@ -746,18 +746,21 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       }
     }
   }
+  // sums over the 4 rows (positions) of the 16 accumulators, transposed: row R ends up
+  // with accumulators 4 R .. 4 R + 3 (head R / 2, dims 8 q16 + 4 (R % 2) + 0..3)
+  float u[4];
+  {
+    float tt[8];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+    for (int j = 0; j < 8; ++j) tt[j] = pack32(acc[0][j], acc[1][j]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = rows4_sum(acc[h][e]);
+    for (int j = 0; j < 4; ++j) u[j] = pack16(tt[j], tt[j + 4]);
+  }
   release_lines(W, W.gl);
   float* rec = &S->apart[W.c][0][0];
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      *(float4*)(rec + h * PART_PER_HEAD + 2 + 8 * q16) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-      *(float4*)(rec + h * PART_PER_HEAD + 2 + 8 * q16 + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-    }
+  {
+    const int R = lane >> 4;
+    *(float4*)(rec + (R >> 1) * PART_PER_HEAD + 2 + 8 * q16 + 4 * (R & 1)) = make_float4(u[0], u[1], u[2], u[3]);
   }
   if (lane == 0) {
     rec[0] = mh[0];
