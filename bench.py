@@ -63,7 +63,7 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(hw, budget_s=12.0, max_steps=24):
+def cpu_baseline(hw, budget_s=12.0, max_steps=400):
     """The fp32 CPU oracle decoding at context ~1921 on this host's cores.
     The oracle's KV cache for positions < 1920 is filled with seeded random
     values (decode time does not depend on them); steps are timed after one
