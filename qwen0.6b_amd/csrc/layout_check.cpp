@@ -69,18 +69,15 @@ int main() {
     for (int m = 0; m < LINES_QKV - LINES_NORM; ++m) CHECK((m >> 1) < QKV_PER_WG, "qkv line");
   }
 
-  // ---- attention input poll: quarter c, lane < 32 -> values 4 (32 c + lane) .. +4 ----
+  // ---- attention input poll: every wave, lane -> q values [4 lane, +4) (slots 2 lane, +1)
+  //      and k | v values [256 + 4 lane, +4) (slots 128 + 2 lane, +1) ----
   {
     std::vector<int> seen(GRP_ROWS, 0);
-    for (int c = 0; c < NCW; ++c)
-      for (int lane = 0; lane < 32; ++lane) {
-        const long slot = 64 * c + (16 * lane) / 8;  // soff / 8 relative to the buffer + voff / 8
+    for (int lane = 0; lane < WAVE; ++lane)
+      for (const int voff : {16 * lane, 1024 + 16 * lane}) {
+        const long slot = voff / 8;
         CHECK(slot % 2 == 0 && slot + 1 < QKV_SLOTS, "att poll range");
-        for (int e = 0; e < 4; ++e) {
-          const int val = 2 * (int)slot + e;
-          CHECK(val == 128 * c + 4 * lane + e, "att vin index");
-          seen[val]++;
-        }
+        for (int e = 0; e < 4; ++e) seen[2 * (int)slot + e]++;
       }
     for (int e = 0; e < GRP_ROWS; ++e) CHECK(seen[e] == 1, "att input %d", e);
   }
@@ -145,14 +142,16 @@ int main() {
     for (int e = 0; e < OCOLS; ++e) CHECK(seen[e] == 1, "combine value %d", e);
   }
 
-  // ---- o_proj: ATTO quarter poll, ring lines, partial rows ----
+  // ---- o_proj: ATTO poll (lane -> values [8 (lane % 32), +8) = slots 4 (lane % 32) .. +3,
+  //      the columns its ring lines hold), ring lines, partial rows ----
   {
     std::vector<int> seen(OCOLS, 0);
-    for (int c = 0; c < NCW; ++c)
-      for (int lane = 0; lane < 16; ++lane) {
-        const int slot = 32 * c + 2 * lane;
-        CHECK(slot + 1 < ATTO_SLOTS, "atto poll");
-        for (int e = 0; e < 4; ++e) seen[64 * c + 4 * lane + e]++;
+    for (int lane = 0; lane < 32; ++lane)
+      for (const int voff : {32 * lane, 32 * lane + 16}) {
+        const int slot = voff / 8;
+        CHECK(slot % 2 == 0 && slot + 1 < ATTO_SLOTS, "atto poll");
+        CHECK(2 * slot >= 8 * lane && 2 * slot + 4 <= 8 * lane + 8, "atto values match the lane's columns");
+        for (int e = 0; e < 4; ++e) seen[2 * slot + e]++;
       }
     for (int e = 0; e < OCOLS; ++e) CHECK(seen[e] == 1, "o input %d", e);
     std::vector<int> rows(HIDDEN * NXCD, 0);
@@ -182,18 +181,20 @@ int main() {
     }
   }
 
-  // ---- residual sums: peer poll addresses ----
+  // ---- residual sums: wave c, lane < 32 polls XCD lane / 4, rows 8 c + 2 (lane % 4), +1 ----
   for (int par = 0; par < 2; ++par)
     for (int i = 0; i < NLOC; ++i)
       for (const long B : {B_OP, B_DP}) {
         std::vector<int> seen(NXCD * HROWS, 0);
         for (int c = 0; c < NCW; ++c) {
-          const long src0 = xbuf(par, 2 * c, B) + HROWS * i;
+          const long src0 = xbuf(par, 0, B) + HROWS * i + 8 * c;
           for (int lane = 0; lane < 32; ++lane) {
-            const long slot = src0 + ((long)((lane >> 4) & 1) * XCD_SLOTS + 2 * (lane & 15));
-            const int g = 2 * c + ((lane >> 4) & 1), r = 2 * (lane & 15);
+            const int g = (lane >> 2) & 7, pr = lane & 3, r = 8 * c + 2 * pr;
+            const long slot = src0 + ((long)g * XCD_SLOTS + 2 * pr);
             CHECK(slot == xbuf(par, g, B) + HROWS * i + r && slot % 2 == 0, "peer poll address");
             CHECK(in_buf(slot, xbuf(par, g, B), HIDDEN) && in_buf(slot + 1, xbuf(par, g, B), HIDDEN), "peer range");
+            // DPP row_ror 8 and 4 sum lanes pr + 4 g' of one 16-lane row; rows 0 and 1 hold g < 4 and g >= 4
+            CHECK(lane / 16 == g / 4 && (lane % 16) / 4 == g % 4, "peer lane placement");
             seen[g * HROWS + r]++;
             seen[g * HROWS + r + 1]++;
           }
@@ -212,18 +213,19 @@ int main() {
           seen[2 * slot + 1]++;
         }
     for (int r = 0; r < HIDDEN; ++r) CHECK(seen[r] == 1, "x row %d", r);
-    // quarter polls of a 1024-value vector: slots 128 c + 2 lane
+    // whole-vector polls of a 1024-value vector: lane -> slots 4 lane .. +3 and 256 + 4 lane .. +3
+    // = values [8 lane, +8) and [512 + 8 lane, +8), the columns of its ring-line bytes
     std::vector<int> got(HIDDEN, 0);
-    for (int c = 0; c < NCW; ++c)
-      for (int lane = 0; lane < WAVE; ++lane) {
-        const int slot = 128 * c + 2 * lane;
-        CHECK(slot + 1 < X_SLOTS, "quarter poll");
-        for (int e = 0; e < 4; ++e) {
-          CHECK(2 * slot + e == 256 * c + 4 * lane + e, "quarter vin index");
-          got[2 * slot + e]++;
-        }
+    for (int lane = 0; lane < WAVE; ++lane)
+      for (const int voff : {32 * lane, 32 * lane + 16, 2048 + 32 * lane, 2048 + 32 * lane + 16}) {
+        const int slot = voff / 8;
+        CHECK(slot % 2 == 0 && slot + 1 < X_SLOTS, "x poll");
+        const int v0 = 2 * slot;
+        CHECK((v0 >= 8 * lane && v0 + 4 <= 8 * lane + 8) || (v0 >= 512 + 8 * lane && v0 + 4 <= 512 + 8 * lane + 8),
+              "x values match the lane's columns");
+        for (int e = 0; e < 4; ++e) got[v0 + e]++;
       }
-    for (int r = 0; r < HIDDEN; ++r) CHECK(got[r] == 1, "quarter value %d", r);
+    for (int r = 0; r < HIDDEN; ++r) CHECK(got[r] == 1, "x value %d", r);
   }
 
   // ---- gate/up rows, INT slots, down input order ----
@@ -242,15 +244,21 @@ int main() {
     // compute wave c: gate rows 3c + jj at lines 2(3c + jj), up at 24 + 2(3c + jj)
     for (int c = 0; c < NCW; ++c)
       for (int jj = 0; jj < 3; ++jj) CHECK(LINES_NORM + 2 * GU_PER_WG + 2 * (3 * c + jj) + 1 < LINES_GU, "gu lines");
-    // INT slots and the down poll: pair k = 32 c + lane -> values 12 (k/4) + 3 (k%4) + {0,1,2}
+    // INT slots: wave c of workgroup i stores slot 8 i + 2 c (values 12 i + 3 c, +1) and
+    // 8 i + 2 c + 1 (value 12 i + 3 c + 2, padding); the down poll gives lane slots 4 lane .. +3
+    // = inter values [6 lane, 6 lane + 6), reshuffled to [8 lane, +8) for lanes < 48
     std::vector<int> seen(ICOLS, 0);
-    for (int c = 0; c < NCW; ++c)
-      for (int lane = 0; lane < 32; ++lane) {
-        const int k = 32 * c + lane, slot = 64 * c + 2 * lane;
-        CHECK(slot == int_slot(k >> 2, k & 3, 0) && slot + 1 == int_slot(k >> 2, k & 3, 1), "int slots");
-        CHECK(slot + 1 < INT_SLOTS, "int range");
-        for (int e = 0; e < 3; ++e) seen[GU_PER_WG * (k >> 2) + 3 * (k & 3) + e]++;
-      }
+    for (int lane = 0; lane < WAVE; ++lane) {
+      const int slot0 = 4 * lane;
+      CHECK(slot0 + 3 < INT_SLOTS, "int range");
+      const int i = lane / 2, c0 = 2 * (lane % 2);
+      CHECK(slot0 == int_slot(i, c0, 0) && slot0 + 1 == int_slot(i, c0, 1) && slot0 + 2 == int_slot(i, c0 + 1, 0) &&
+                slot0 + 3 == int_slot(i, c0 + 1, 1),
+            "int slots");
+      // values carried: 12 i + 3 c0 + {0, 1, 2}, 12 i + 3 (c0 + 1) + {0, 1, 2} == 6 lane + {0..5}
+      CHECK(GU_PER_WG * i + 3 * c0 == 6 * lane, "int lane values");
+      for (int e = 0; e < 6; ++e) seen[6 * lane + e]++;
+    }
     for (int e = 0; e < ICOLS; ++e) CHECK(seen[e] == 1, "inter value %d", e);
     // down ring lines: row 32 i + m, columns 384 x + 8 ln (ln < 48)
     std::vector<int> rows(HIDDEN * NXCD, 0);

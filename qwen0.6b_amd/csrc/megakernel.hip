@@ -59,11 +59,13 @@ constexpr int DMA_DEPTH = 16;  // LDS-DMA lines a loader wave keeps in flight
 constexpr int TRACE_EVENTS = 6;
 enum TraceEvent : int {
   TR_POLL = 0,   // compute wave 0 starts waiting for the stage input
-  TR_INPUT = 1,  // compute wave 0 has its quarter of the input
-  TR_SYNC = 2,   // compute wave 0 passed the compute-wave barrier (whole input in LDS)
-  TR_STORE = 3,  // compute wave 0 stored its results
-  TR_LINES = 4,  // compute wave 0 has the stage's weight / K-V lines in the ring
-  TR_MERGE = 5,  // attention: compute wave 0 passed the barrier before the split merge
+  TR_INPUT = 1,  // compute wave 0 has the stage input
+  TR_SYNC = 2,   // lm_head stage: compute wave 0 finished its lm_head rows
+  TR_STORE = 3,  // compute wave 0 stored its results (and they were acknowledged)
+  TR_LINES = 4,  // layer stages: compute wave 0 has the stage's ring lines;
+                 // lm_head stage: compute wave 0 has the argmax partials of all workgroups
+  TR_MERGE = 5,  // attention: compute wave 0 passed the barrier before the split merge;
+                 // lm_head stage: loader wave 0 finished its lm_head rows
 };
 QL_HD int trace_stages(int L) { return NSTAGE * L + 1; }
 
@@ -273,8 +275,8 @@ struct Shared {
   v4u ring[RING_LINES][LINE_BYTES / 16];  // 128 KB weight / K-V line ring (must stay first: LDS offset 0)
   float wbuf[NCW][4 * HD];          // per-wave scratch: roped q | k | v (attention), down-input reshuffle
   float apart[NCW][2][PART_PER_HEAD];  // per-wave attention partials (m, l, acc)
-  float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32) (compute wave 0 only)
-  float actres[HROWS];             // fp32 post-attention residual, same rows (compute wave 0 only)
+  float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32) (wave c: rows 8 c .. 8 c + 7)
+  float actres[HROWS];             // fp32 post-attention residual, same rows and owners
   float xfin[HIDDEN];              // lm_head input (fp32)
   float lmv[NCW + NLW];            // per-wave lm_head best value
   int lmi[NCW + NLW];              // per-wave lm_head best row
@@ -586,10 +588,13 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   if (l == 0) {
     const _Float16* row = P.embed + (long)token * HIDDEN;
     ss = load_x1024(row, lane, xa, xb);
-    if (W.c == 0 && lane < HROWS) S->resid[lane] = (float)row[HROWS * W.i + lane];
+    if (lane < 8) S->resid[8 * W.c + lane] = (float)row[HROWS * W.i + 8 * W.c + lane];
     wait_lines(W, W.gl);
   } else {
-    ss = poll_x1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), xa, xb, [&] { wait_lines(W, W.gl); });
+    ss = poll_x1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), xa, xb, [&] {
+      wait_lines(W, W.gl);
+      trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
+    });
   }
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
   float a[8], b[8];
@@ -627,7 +632,10 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     const int voff[2] = {16 * lane, 1024 + 16 * lane};
     v4u v[2];
     poll<2>(W.C, tag_of(epoch, l, S_QKV), voff, (int)(xbuf(par, W.x, B_QKV) * 8), true, v,
-            [&] { wait_lines(W, W.gl); });
+            [&] {
+      wait_lines(W, W.gl);
+      trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
+    });
     qv = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
     kv = make_float4(lo_h(v[1].x), hi_h(v[1].x), lo_h(v[1].z), hi_h(v[1].z));
   }
@@ -855,7 +863,10 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
     const int voff[2] = {32 * (lane & 31), 32 * (lane & 31) + 16};
     v4u v[2];
     poll<2>(W.C, tag_of(epoch, l, S_COMB), voff, (int)(xbuf(par, W.x, B_ATTO) * 8), true, v,
-            [&] { wait_lines(W, W.gl); });
+            [&] {
+      wait_lines(W, W.gl);
+      trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
+    });
     unpack8(v[0], v[1], a);
   }
   trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
@@ -876,52 +887,48 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   trace_ev(P, t, NSTAGE * l + S_O, TR_STORE);
 }
 
-// sum of the 8 per-XCD partials of rows [32 i, 32 i + 32) plus the residual, by
-// compute wave 0 alone (the other waves go on to the next stage's poll); `src` is
-// B_OP (o_proj, producing the post-attention residual) or B_DP (down, producing the
-// next layer's residual)
+// sum of the 8 per-XCD partials plus the residual: compute wave c owns rows
+// [32 i + 8 c, +8) and their fp32 residual; `src` is B_OP (o_proj, producing the
+// post-attention residual) or B_DP (down, producing the next layer's residual)
 __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u32 epoch, bool is_down) {
-  if (W.c != 0) return;
   Shared* S = W.C.S;
   const int lane = W.lane, par = l & 1;
   const int st = is_down ? S_DSUM : S_OSUM;
-  const int q = lane & 7;  // rows 4 q .. 4 q + 3
+  const int pr = lane & 3;  // rows 8 c + 2 pr, +1
   trace_ev(P, t, NSTAGE * l + st, TR_POLL);
-  float y[4];
-  {  // lane: XCD lane / 8, rows 4 q .. 4 q + 3
-    const long src0 = xbuf(par, 0, is_down ? B_DP : B_OP) + HROWS * W.i;
-    const int off = (int)(((long)(lane >> 3) * XCD_SLOTS + 4 * q) * 8);
-    const int voff[2] = {off, off + 16};
-    v4u v[2];
-    poll<2>(W.C, tag_of(epoch, l, is_down ? S_DOWN : S_O), voff, (int)(src0 * 8), true, v);
-    y[0] = __uint_as_float(v[0].x);
-    y[1] = __uint_as_float(v[0].z);
-    y[2] = __uint_as_float(v[1].x);
-    y[3] = __uint_as_float(v[1].z);
+  float y0, y1;
+  {  // lanes 0-31: XCD lane / 4, rows 8 c + 2 pr, +1
+    const long src0 = xbuf(par, 0, is_down ? B_DP : B_OP) + HROWS * W.i + 8 * W.c;
+    const int voff[1] = {(int)(((long)((lane >> 2) & 7) * XCD_SLOTS + 2 * pr) * 8)};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, is_down ? S_DOWN : S_O), voff, (int)(src0 * 8), lane < 32, v);
+    y0 = __uint_as_float(v[0].x);  // lanes 32-63 hold 0
+    y1 = __uint_as_float(v[0].z);
   }
   trace_ev(P, t, NSTAGE * l + st, TR_INPUT);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {  // over the 8 XCDs: lanes q, q + 8, ..., q + 56
-    y[e] += dpp<ROR8>(y[e]);
-    y[e] = rows4_sum(y[e]);
-  }
-  if (lane < 8) {
+  // over the 8 XCDs: lanes pr + 4 g (g = 0..3 in each 16-lane row), then rows 0 + 1
+  y0 += dpp<ROR8>(y0);
+  y1 += dpp<ROR8>(y1);
+  y0 += dpp<ROR4>(y0);
+  y1 += dpp<ROR4>(y1);
+  y0 = pack16(y0, y0);
+  y1 = pack16(y1, y1);
+  if (lane < 4) {
+    const int r = 8 * W.c + 2 * pr;
     float* res = is_down ? S->actres : S->resid;  // input residual
     float* out = is_down ? S->resid : S->actres;
-    const float4 r = *(const float4*)(res + 4 * q);
-    const float s0 = y[0] + r.x, s1 = y[1] + r.y, s2 = y[2] + r.z, s3 = y[3] + r.w;
-    *(float4*)(out + 4 * q) = make_float4(s0, s1, s2, s3);
-    const int row = HROWS * W.i + 4 * q;
+    const float2 rv = *(const float2*)(res + r);
+    const float s0 = y0 + rv.x, s1 = y1 + rv.y;
+    *(float2*)(out + r) = make_float2(s0, s1);
+    const int row = HROWS * W.i + r;
     if (P.mode == MODE_MLP) {
-      if (W.x == 0) *(float4*)(P.out_vec + row) = make_float4(s0, s1, s2, s3);
+      if (W.x == 0) *(float2*)(P.out_vec + row) = make_float2(s0, s1);
     } else {
-      const long slot = xbuf(par, W.x, is_down ? B_X : B_ACT) + 16 * W.i + 2 * q;
-      ll_store_xcd(P.ws, slot, pack_h2(s0, s1), tag_of(epoch, l, st));
-      ll_store_xcd(P.ws, slot + 1, pack_h2(s2, s3), tag_of(epoch, l, st));
+      ll_store_xcd(P.ws, xbuf(par, W.x, is_down ? B_X : B_ACT) + row / 2, pack_h2(s0, s1), tag_of(epoch, l, st));
       if (is_down && l == P.num_layers - 1 && W.x == 0) {  // final-layer residual
-        if (P.hidden_steps) *(float4*)(P.hidden_steps + (long)t * HIDDEN + row) = make_float4(s0, s1, s2, s3);
-        const h4 ho = {(_Float16)s0, (_Float16)s1, (_Float16)s2, (_Float16)s3};
-        *(h4*)(P.hidden_out + row) = ho;
+        if (P.hidden_steps) *(float2*)(P.hidden_steps + (long)t * HIDDEN + row) = make_float2(s0, s1);
+        const h2 ho = {(_Float16)s0, (_Float16)s1};
+        *(h2*)(P.hidden_out + row) = ho;
       }
     }
   }
@@ -939,10 +946,13 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   float xa[8], xb[8], ss;
   if (P.mode == MODE_MLP) {
     ss = load_x1024(P.in_vec, lane, xa, xb);
-    if (W.c == 0 && lane < HROWS) S->actres[lane] = (float)P.in_vec[HROWS * W.i + lane];
+    if (lane < 8) S->actres[8 * W.c + lane] = (float)P.in_vec[HROWS * W.i + 8 * W.c + lane];
     wait_lines(W, W.gl);
   } else {
-    ss = poll_x1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), xa, xb, [&] { wait_lines(W, W.gl); });
+    ss = poll_x1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), xa, xb, [&] {
+      wait_lines(W, W.gl);
+      trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
+    });
   }
   trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
   float a[8], b[8];
@@ -985,7 +995,10 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
     const int voff[2] = {32 * lane, 32 * lane + 16};
     v4u v[2];
     poll<2>(W.C, tag_of(epoch, l, S_GU), voff, (int)(xbuf(par, W.x, B_INT) * 8), true, v,
-            [&] { wait_lines(W, W.gl); });
+            [&] {
+      wait_lines(W, W.gl);
+      trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
+    });
     float* d = S->wbuf[W.c];
     *(float2*)(d + 6 * lane) = make_float2(lo_h(v[0].x), hi_h(v[0].x));
     *(float2*)(d + 6 * lane + 2) = make_float2(lo_h(v[0].z), lo_h(v[1].x));
@@ -1085,6 +1098,7 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
     st_lm_input(W, P, t, epoch);
     ++phase;
     lm_rows(W.C, P, c, t, phase);
+    trace_ev(P, t, NSTAGE * L, TR_SYNC);
     // workgroup partial -> ARG slots; every workgroup then reduces all 256
     if (c == 0) {
       lds_wait_ge(W.C, &S->lm_cnt, (NCW + NLW) * phase);
@@ -1102,6 +1116,7 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
       const int voff[1] = {16 * W.lane};
       v4u v[1];
       poll<1>(W.C, tag_arg(epoch), voff, (int)(slot_arg(t & 1, 128 * c) * 8), true, v);
+      trace_ev(P, t, NSTAGE * L, TR_LINES);
       float best = __uint_as_float(v[0].x);
       int bidx = (int)v[0].z;
       wave_argmax(best, bidx);
@@ -1249,6 +1264,7 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
     if (P.mode == MODE_MLP) break;
     ++phase;
     lm_rows(C, P, NCW + q, t, phase);
+    if (q == 0) trace_ev(P, t, NSTAGE * L, TR_MERGE);
   }
   if (!C.ok) lds_st(&S->abort, 1u);
 }
