@@ -132,12 +132,15 @@ int main() {
       const int hh = i / 16, d0 = 8 * (i % 16);
       for (int e = 0; e < 8; ++e) seen[hh * HD + d0 + e]++;
       CHECK(8 * i == hh * HD + d0, "ATTO value order");
-      for (int s = 0; s < NSPLIT; ++s)
-        for (int k = 0; k < 5; ++k) {
-          const long slot = part_index(s, hh, k == 0 ? 0 : 2 + d0 + 2 * (k - 1));
-          CHECK(slot % 2 == 0 && slot + 1 < PART_SLOTS, "combine poll");
-        }
-      for (int lane = 0; lane < 4; ++lane) CHECK(4 * i + lane < ATTO_SLOTS, "atto slot");
+      // wave c merges dims d0 + 2 c, +1: lane s < 32 polls (m, l) and that dim pair of split s
+      for (int c = 0; c < NCW; ++c) {
+        for (int s = 0; s < NSPLIT; ++s)
+          for (const int e : {0, 2 + d0 + 2 * c}) {
+            const long slot = part_index(s, hh, e);
+            CHECK(slot % 2 == 0 && slot + 1 < PART_SLOTS, "combine poll");
+          }
+        CHECK(4 * i + c < ATTO_SLOTS && 2 * (4 * i + c) == hh * HD + d0 + 2 * c, "atto slot");
+      }
     }
     for (int e = 0; e < OCOLS; ++e) CHECK(seen[e] == 1, "combine value %d", e);
   }

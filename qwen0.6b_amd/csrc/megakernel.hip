@@ -812,41 +812,26 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
 }
 
-// combine (wave 0): q head 2x + i / 16, dims [8 (i % 16), +8) over the 32 splits
+// combine: q head 2x + i / 16; compute wave c merges dims d0 + 2 c, +1 (d0 = 8 (i % 16))
+// over the 32 split partials of the kv head (lane < 32: split lane)
 __device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u32 epoch) {
-  if (W.c != 0) return;
   const int lane = W.lane, par = l & 1;
-  const int hh = W.i / 16, d0 = 8 * (W.i % 16);
+  const int hh = W.i / 16, d = 8 * (W.i % 16) + 2 * W.c;
   const int s = lane & 31;
-  int voff[5];
-#pragma unroll
-  for (int k = 0; k < 5; ++k) voff[k] = (int)(part_index(s, hh, k == 0 ? 0 : 2 + d0 + 2 * (k - 1)) * 8);
-  v4u v[5];
+  const int voff[2] = {(int)(part_index(s, hh, 0) * 8), (int)(part_index(s, hh, 2 + d) * 8)};
+  v4u v[2];
   trace_ev(P, t, NSTAGE * l + S_COMB, TR_POLL);
-  poll<5>(W.C, tag_of(epoch, l, S_ATT), voff, (int)(xbuf(par, W.x, B_PART) * 8), lane < NSPLIT, v);
+  poll<2>(W.C, tag_of(epoch, l, S_ATT), voff, (int)(xbuf(par, W.x, B_PART) * 8), lane < NSPLIT, v);
   trace_ev(P, t, NSTAGE * l + S_COMB, TR_INPUT);
-  float m = -INFINITY, lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (lane < NSPLIT) {
-    m = __uint_as_float(v[0].x);
-    lsum = __uint_as_float(v[0].z);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      acc[2 * k] = __uint_as_float(v[k + 1].x);
-      acc[2 * k + 1] = __uint_as_float(v[k + 1].z);
-    }
-  }
-  const float M = max16x(row16_max(m));  // over lanes 0-31 (lanes >= 32 hold -inf)
+  const float m = lane < NSPLIT ? __uint_as_float(v[0].x) : -INFINITY;  // lanes >= 32 hold 0
+  const float M = max16x(row16_max(m));  // over lanes 0-31
   const float e = (lane < NSPLIT && m != -INFINITY) ? __expf(m - M) : 0.f;
-  const float Lt = half_sum(e * lsum);
-  float o[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) o[k] = half_sum(e * acc[k]);
+  const float Lt = half_sum(e * __uint_as_float(v[0].z));
+  const float oa = half_sum(e * __uint_as_float(v[1].x));
+  const float ob = half_sum(e * __uint_as_float(v[1].z));
   const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-  // lane k < 4 stores dims 2k, 2k+1 (static selects: no lane-indexed array)
-  const float oa = lane == 0 ? o[0] : (lane == 1 ? o[2] : (lane == 2 ? o[4] : o[6]));
-  const float ob = lane == 0 ? o[1] : (lane == 1 ? o[3] : (lane == 2 ? o[5] : o[7]));
-  if (lane < 4)
-    ll_store_xcd(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + lane, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
+  if (lane == 0)
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + W.c, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
   drain_stores(S_COMB);
   trace_ev(P, t, NSTAGE * l + S_COMB, TR_STORE);
 }
