@@ -153,6 +153,50 @@ def test_full_model_golden_tokens_free_running(ext, full, qa):
     assert dec.position == len(gold["prompt"]) - 1 + 4
 
 
+def test_c3_prompt128_generate512(ext, full, qa):
+    """C3: 128-id prompt (seed 1) prefilled, then generate_nosync of 512 tokens
+    (positions 127..638), 28 layers, free running. The oracle is teacher forced
+    along the engine's own sequence, so every one of the 512 greedy choices is
+    checked (near-ties exempt); logits and hidden state are compared every 16th
+    step through a teacher-forced generate_ex run over the same ids."""
+    hw, w, packed = full
+    prompt = qw.synthetic_prompt(128, seed=1)
+    n_new = 512
+    dec = qa.Decoder(weights=w, verbose=False)
+    gen = dec.generate_ids(prompt, n_new)
+    assert len(gen) == n_new and dec.position == len(prompt) - 1 + n_new
+    ids = prompt + gen[:-1]  # inputs of positions 0 .. 638
+    first = len(prompt) - 1
+    sample = set(range(first, len(ids), 16)) | {len(ids) - 1}
+    oracle = orc.Oracle(hw)
+    ref, ref_at = [], {}
+    for p, tok in enumerate(ids):
+        st = oracle.step(tok, p, want_logits=p >= first)
+        if p >= first:
+            st["gap"] = orc.top2_gap(st["logits"])
+            ref.append({"token": st["token"], "gap": st["gap"]})
+            if p in sample:
+                ref_at[p] = st
+    exempt = 0
+    for s, st in enumerate(ref):
+        if st["gap"] >= GAP_EXEMPT:
+            assert gen[s] == st["token"], f"c3 step {s}: token {gen[s]} != {st['token']}"
+        else:
+            exempt += 1
+    run = Run(w, packed, 28)
+    toks, logits, hidden = run.forced(ext, ids, 0)
+    assert toks[first:] == gen, "teacher-forced run differs from the free-running one"
+    worst_l = worst_h = 0.0
+    for p, st in ref_at.items():
+        dl = float((logits[p] - st["logits"]).abs().max())
+        dh = float((hidden[p] - st["hidden"]).abs().max())
+        worst_l, worst_h = max(worst_l, dl), max(worst_h, dh)
+        assert dl <= TOL_LOGITS, f"c3 position {p}: logits max-abs {dl}"
+        assert dh <= TOL_HIDDEN, f"c3 position {p}: hidden max-abs {dh}"
+    print(f"c3: {n_new} tokens checked ({exempt} near-tie steps exempt), {len(ref_at)} positions: "
+          f"worst logits {worst_l:.3e}, worst hidden {worst_h:.3e}")
+
+
 def test_long_context_two_layers(ext, full, qa):
     """Attention at the longest contexts: a 2-layer model prefilled to position
     2038, then 10 teacher-forced steps up to the last cache slot (ctx 2048)."""
