@@ -115,6 +115,18 @@ __device__ __forceinline__ float dot8(v4u w, const float (&a)[8]) {
   return s;
 }
 
+// 8 fp16 weights dotted with 8 fp16 activations (v_dot2_f32_f16: exact products, fp32 sums).
+// The whole 16 bytes are reinterpreted once and split by swizzle: bit-casting a single
+// element expression such as `w.y` compiles to the `.x` element with this toolchain.
+__device__ __forceinline__ float dot8h(v4u w, v4u a) {
+  const h8 wh = __builtin_bit_cast(h8, w), ah = __builtin_bit_cast(h8, a);
+  float s = __builtin_amdgcn_fdot2(wh.s01, ah.s01, 0.f, false);
+  s = __builtin_amdgcn_fdot2(wh.s23, ah.s23, s, false);
+  s = __builtin_amdgcn_fdot2(wh.s45, ah.s45, s, false);
+  s = __builtin_amdgcn_fdot2(wh.s67, ah.s67, s, false);
+  return s;
+}
+
 // ---- cross-lane reductions ---------------------------------------------------------
 // A wave is 4 rows of 16 lanes. Within a row: DPP row_ror (folded into v_add/v_max).
 // Across rows: gfx950 v_permlane16_swap (rows 0<->1, 2<->3) and v_permlane32_swap
@@ -620,7 +632,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   const int lane = W.lane, par = l & 1;
   const int pos = P.start_pos + t, ctx = pos + 1;
   const int d4 = 4 * (lane & 31);
-  float* qr = S->wbuf[W.c];
+  _Float16* qr = (_Float16*)S->wbuf[W.c];  // roped q0 | q1 | k | v of the current position (fp16)
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_POLL);
   // ring: line n0 = q_norm | k_norm | cos[pos] | sin[pos]; K lines n0 + 1 + m; V lines n0 + 1 + nk + m
   const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
@@ -668,45 +680,31 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       qo[j] = qq[j] * cs + qp * sn;
       ko[j] = kk[j] * cs + kp * sn;
     }
-    *(float4*)(qr + 4 * lane) = make_float4(qo[0], qo[1], qo[2], qo[3]);
-    if (lane < 32)
-      *(float4*)(qr + 256 + 4 * lane) = make_float4(ko[0], ko[1], ko[2], ko[3]);
-    else
-      *(float4*)(qr + 256 + 4 * lane) = make_float4(k[0], k[1], k[2], k[3]);
+    // fp16, as the values the cache keeps (and as the reference rounds q)
+    const h4 qh = {(_Float16)qo[0], (_Float16)qo[1], (_Float16)qo[2], (_Float16)qo[3]};
+    const h4 kvh = lane < 32 ? h4{(_Float16)ko[0], (_Float16)ko[1], (_Float16)ko[2], (_Float16)ko[3]}
+                             : h4{(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
+    *(h4*)(qr + 4 * lane) = qh;
+    *(h4*)(qr + 256 + 4 * lane) = kvh;
     // the split holding `pos` writes this position's K (roped) and V to the cache
     if (W.c == 0 && att_t0(ctx, W.i) <= pos && pos < att_t1(ctx, W.i)) {
       const long row = (((long)l * NKV + W.x) * P.max_seq + pos) * HD + d4;
-      if (lane < 32) {
-        const h4 o = {(_Float16)ko[0], (_Float16)ko[1], (_Float16)ko[2], (_Float16)ko[3]};
-        *(h4*)(P.k_cache + row) = o;
-      } else {
-        const h4 o = {(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
-        *(h4*)(P.v_cache + row) = o;
-      }
+      *(h4*)((lane < 32 ? P.k_cache : P.v_cache) + row) = kvh;
     }
   }
   // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..
   const int j = lane >> 4, q16 = lane & 15;
-  float qa[8], qb[8];
-  {
-    const float4 a0 = *(const float4*)(qr + 8 * q16), a1 = *(const float4*)(qr + 8 * q16 + 4);
-    const float4 b0 = *(const float4*)(qr + 128 + 8 * q16), b1 = *(const float4*)(qr + 128 + 8 * q16 + 4);
-    qa[0] = a0.x; qa[1] = a0.y; qa[2] = a0.z; qa[3] = a0.w; qa[4] = a1.x; qa[5] = a1.y; qa[6] = a1.z; qa[7] = a1.w;
-    qb[0] = b0.x; qb[1] = b0.y; qb[2] = b0.z; qb[3] = b0.w; qb[4] = b1.x; qb[5] = b1.y; qb[6] = b1.z; qb[7] = b1.w;
-  }
+  // the scratch was written as fp16 vectors of another type: keep the compiler from
+  // moving these reads above those writes (type-based alias analysis would allow it)
+  asm volatile("" ::: "memory");
+  const v4u qa = *(const v4u*)(qr + 8 * q16), qb = *(const v4u*)(qr + 128 + 8 * q16);  // q heads 0, 1 (fp16)
   // the current position is not in the cache lines (the loader reads a spare row for it):
   // the wave whose 16 positions include it writes its fp16 k and v into its own ring lines
   {
     const int mp = (pos - t0) >> 2, jp = (pos - t0) & 3;
     if (pos >= t0 && pos < t1 && (mp >> 2) == W.c && j == jp) {
-      const float4 k0 = *(const float4*)(qr + 256 + 8 * q16), k1 = *(const float4*)(qr + 256 + 8 * q16 + 4);
-      const float4 v0 = *(const float4*)(qr + 384 + 8 * q16), v1 = *(const float4*)(qr + 384 + 8 * q16 + 4);
-      const h8 kh = {(_Float16)k0.x, (_Float16)k0.y, (_Float16)k0.z, (_Float16)k0.w,
-                     (_Float16)k1.x, (_Float16)k1.y, (_Float16)k1.z, (_Float16)k1.w};
-      const h8 vh = {(_Float16)v0.x, (_Float16)v0.y, (_Float16)v0.z, (_Float16)v0.w,
-                     (_Float16)v1.x, (_Float16)v1.y, (_Float16)v1.z, (_Float16)v1.w};
-      S->ring[(nkl + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, kh);
-      S->ring[(nkl + nk + mp) % RING_LINES][lane] = __builtin_bit_cast(v4u, vh);
+      S->ring[(nkl + mp) % RING_LINES][lane] = *(const v4u*)(qr + 256 + 8 * q16);
+      S->ring[(nkl + nk + mp) % RING_LINES][lane] = *(const v4u*)(qr + 384 + 8 * q16);
     }
   }
   float sc[4][2];
@@ -718,8 +716,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     float s0 = 0.f, s1 = 0.f;
     if (m < nk) {
       const v4u kw = ring_line(S, nkl + m)[lane];
-      s0 = dot8(kw, qa);
-      s1 = dot8(kw, qb);
+      s0 = dot8h(kw, qa);
+      s1 = dot8h(kw, qb);
     }
     s0 = row16_sum(s0) * P.attn_scale;
     s1 = row16_sum(s1) * P.attn_scale;
@@ -989,6 +987,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
     *(float2*)(d + 6 * lane + 2) = make_float2(lo_h(v[0].z), lo_h(v[1].x));
     *(float2*)(d + 6 * lane + 4) = make_float2(hi_h(v[1].x), lo_h(v[1].z));
     const int o = lane < 48 ? 8 * lane : 0;
+    asm volatile("" ::: "memory");  // reads of other lanes' writes, through another vector type
     const float4 a0 = *(const float4*)(d + o), a1 = *(const float4*)(d + o + 4);
     const float z = lane < 48 ? 1.f : 0.f;  // lanes 48-63 contribute nothing
     a[0] = a0.x * z; a[1] = a0.y * z; a[2] = a0.z * z; a[3] = a0.w * z;
