@@ -60,7 +60,8 @@ constexpr int TRACE_EVENTS = 6;
 enum TraceEvent : int {
   TR_POLL = 0,   // compute wave 0 starts waiting for the stage input
   TR_INPUT = 1,  // compute wave 0 has the stage input
-  TR_SYNC = 2,   // lm_head stage: compute wave 0 finished its lm_head rows
+  TR_SYNC = 2,   // attention: the wave's partial is in LDS (before the merge barrier);
+                 // lm_head stage: compute wave 0 finished its lm_head rows
   TR_STORE = 3,  // compute wave 0 stored its results (and they were acknowledged)
   TR_LINES = 4,  // layer stages: compute wave 0 has the stage's ring lines;
                  // lm_head stage: compute wave 0 has the argmax partials of all workgroups
@@ -774,6 +775,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     rec[PART_PER_HEAD] = mh[1];
     rec[PART_PER_HEAD + 1] = lh[1];
   }
+  trace_ev(P, t, NSTAGE * l + S_ATT, TR_SYNC);
   sync4(W);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_MERGE);
   // merge the 4 wave partials: wave c writes entries [65 c, 65 c + 65) of the 260
