@@ -69,15 +69,19 @@ int main() {
     for (int m = 0; m < LINES_QKV - LINES_NORM; ++m) CHECK((m >> 1) < QKV_PER_WG, "qkv line");
   }
 
-  // ---- attention input poll: every wave, lane -> q values [4 lane, +4) (slots 2 lane, +1)
-  //      and k | v values [256 + 4 lane, +4) (slots 128 + 2 lane, +1) ----
+  // ---- attention input poll: wave c, lane < 32 -> slots 64 c + 2 lane, +1 = values
+  //      128 c + 4 lane .. +4, gathered in LDS; every lane then reads q values [4 lane, +4)
+  //      and k | v values [256 + 4 lane, +4) ----
   {
     std::vector<int> seen(GRP_ROWS, 0);
-    for (int lane = 0; lane < WAVE; ++lane)
-      for (const int voff : {16 * lane, 1024 + 16 * lane}) {
-        const long slot = voff / 8;
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < 32; ++lane) {
+        const long slot = 64 * c + (16 * lane) / 8;  // (soff + voff) / 8 relative to the buffer
         CHECK(slot % 2 == 0 && slot + 1 < QKV_SLOTS, "att poll range");
-        for (int e = 0; e < 4; ++e) seen[2 * (int)slot + e]++;
+        for (int e = 0; e < 4; ++e) {
+          CHECK(2 * (int)slot + e == 128 * c + 4 * lane + e, "att gather index");
+          seen[2 * (int)slot + e]++;
+        }
       }
     for (int e = 0; e < GRP_ROWS; ++e) CHECK(seen[e] == 1, "att input %d", e);
   }
@@ -216,17 +220,17 @@ int main() {
           seen[2 * slot + 1]++;
         }
     for (int r = 0; r < HIDDEN; ++r) CHECK(seen[r] == 1, "x row %d", r);
-    // whole-vector polls of a 1024-value vector: lane -> slots 4 lane .. +3 and 256 + 4 lane .. +3
-    // = values [8 lane, +8) and [512 + 8 lane, +8), the columns of its ring-line bytes
+    // quarter polls of a 1024-value vector: wave c, lane -> slots 128 c + 2 lane, +1 =
+    // values 256 c + 4 lane .. +4, gathered in LDS; lanes then read [8 lane, +8) and [512 + 8 lane, +8)
     std::vector<int> got(HIDDEN, 0);
-    for (int lane = 0; lane < WAVE; ++lane)
-      for (const int voff : {32 * lane, 32 * lane + 16, 2048 + 32 * lane, 2048 + 32 * lane + 16}) {
-        const int slot = voff / 8;
-        CHECK(slot % 2 == 0 && slot + 1 < X_SLOTS, "x poll");
-        const int v0 = 2 * slot;
-        CHECK((v0 >= 8 * lane && v0 + 4 <= 8 * lane + 8) || (v0 >= 512 + 8 * lane && v0 + 4 <= 512 + 8 * lane + 8),
-              "x values match the lane's columns");
-        for (int e = 0; e < 4; ++e) got[v0 + e]++;
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < WAVE; ++lane) {
+        const int slot = 128 * c + 2 * lane;
+        CHECK(slot + 1 < X_SLOTS, "x poll");
+        for (int e = 0; e < 4; ++e) {
+          CHECK(2 * slot + e == 256 * c + 4 * lane + e, "x gather index");
+          got[2 * slot + e]++;
+        }
       }
     for (int r = 0; r < HIDDEN; ++r) CHECK(got[r] == 1, "x value %d", r);
   }
@@ -247,21 +251,16 @@ int main() {
     // compute wave c: gate rows 3c + jj at lines 2(3c + jj), up at 24 + 2(3c + jj)
     for (int c = 0; c < NCW; ++c)
       for (int jj = 0; jj < 3; ++jj) CHECK(LINES_NORM + 2 * GU_PER_WG + 2 * (3 * c + jj) + 1 < LINES_GU, "gu lines");
-    // INT slots: wave c of workgroup i stores slot 8 i + 2 c (values 12 i + 3 c, +1) and
-    // 8 i + 2 c + 1 (value 12 i + 3 c + 2, padding); the down poll gives lane slots 4 lane .. +3
-    // = inter values [6 lane, 6 lane + 6), reshuffled to [8 lane, +8) for lanes < 48
+    // INT slots and the down poll: wave c, lane < 32 -> pair k = 32 c + lane (slots 2 k, 2 k + 1)
+    // = workgroup k / 4, wave k % 4: values 12 (k / 4) + 3 (k % 4) + {0, 1, 2}, gathered in LDS
     std::vector<int> seen(ICOLS, 0);
-    for (int lane = 0; lane < WAVE; ++lane) {
-      const int slot0 = 4 * lane;
-      CHECK(slot0 + 3 < INT_SLOTS, "int range");
-      const int i = lane / 2, c0 = 2 * (lane % 2);
-      CHECK(slot0 == int_slot(i, c0, 0) && slot0 + 1 == int_slot(i, c0, 1) && slot0 + 2 == int_slot(i, c0 + 1, 0) &&
-                slot0 + 3 == int_slot(i, c0 + 1, 1),
-            "int slots");
-      // values carried: 12 i + 3 c0 + {0, 1, 2}, 12 i + 3 (c0 + 1) + {0, 1, 2} == 6 lane + {0..5}
-      CHECK(GU_PER_WG * i + 3 * c0 == 6 * lane, "int lane values");
-      for (int e = 0; e < 6; ++e) seen[6 * lane + e]++;
-    }
+    for (int c = 0; c < NCW; ++c)
+      for (int lane = 0; lane < 32; ++lane) {
+        const int k = 32 * c + lane, slot = 64 * c + 2 * lane;
+        CHECK(slot == int_slot(k >> 2, k & 3, 0) && slot + 1 == int_slot(k >> 2, k & 3, 1), "int slots");
+        CHECK(slot + 1 < INT_SLOTS, "int range");
+        for (int e = 0; e < 3; ++e) seen[GU_PER_WG * (k >> 2) + 3 * (k & 3) + e]++;
+      }
     for (int e = 0; e < ICOLS; ++e) CHECK(seen[e] == 1, "inter value %d", e);
     // down ring lines: row 32 i + m, columns 384 x + 8 ln (ln < 48)
     std::vector<int> rows(HIDDEN * NXCD, 0);

@@ -286,7 +286,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 struct Shared {
   v4u ring[RING_LINES][LINE_BYTES / 16];  // 128 KB weight / K-V line ring (must stay first: LDS offset 0)
-  float wbuf[NCW][4 * HD];          // per-wave scratch: roped q | k | v (attention), down-input reshuffle
+  float wbuf[NCW][2 * HD];          // per-wave scratch: the roped fp16 q0 | q1 | k | v of attention
+  float xs[HIDDEN];                // QKV / gate-up input vector, gathered from the four waves' quarters
+  float xss[2][NCW];               // the quarters' sums of squares (alternating)
   float apart[NCW][2][PART_PER_HEAD];  // per-wave attention partials (m, l, acc)
   float resid[HROWS];              // fp32 residual x, rows [32 i, 32 i + 32) (wave c: rows 8 c .. 8 c + 7)
   float actres[HROWS];             // fp32 post-attention residual, same rows and owners
@@ -532,9 +534,11 @@ __device__ __forceinline__ void release_lines(CW& W, u32 end) {
   if (W.lane == 0) lds_st(&W.C.S->cons[W.c], end);
 }
 
-// Stage inputs go straight from the exchange slots into each compute wave's
-// registers: every wave polls the whole vector it needs, so no stage waits for the
-// workgroup's other waves before it computes.
+// Stage inputs: small ones (attention output, split partials, residual partials) go
+// straight from the exchange slots into each compute wave's registers, every wave
+// polling what it needs; the larger vectors (x, q|k|v, SiLU*up) are polled one quarter
+// per wave and gathered in LDS behind one four-wave barrier, which keeps each XCD's
+// polling traffic a quarter as large.
 
 // slots (2 s, 2 s + 1) of a b128 pair -> values 4 s .. 4 s + 3 of an H2 vector
 __device__ __forceinline__ void unpack8(v4u p, v4u q, float (&x)[8]) {
@@ -548,16 +552,28 @@ __device__ __forceinline__ float sumsq16(const float (&xa)[8], const float (&xb)
   return s;
 }
 // the lane's values x[8 lane, +8) and x[512 + 8 lane, +8) of a 1024-value H2 vector in
-// slots [base_slot, base_slot + 512); returns their sum of squares
+// slots [base_slot, base_slot + 512); returns the whole vector's sum of squares. Each wave
+// polls one quarter (1 KB): polling the whole 4 KB from all 128 waves of an XCD costs
+// 2.5x as long per hand-off (measured 1.10 vs 0.43 us per all-gather round)
 template <typename Pre>
 __device__ __forceinline__ float poll_x1024(CW& W, u32 tag, long base_slot, float (&xa)[8], float (&xb)[8], Pre first) {
-  const int lane = W.lane;
-  const int voff[4] = {32 * lane, 32 * lane + 16, 2048 + 32 * lane, 2048 + 32 * lane + 16};
-  v4u v[4];
-  poll<4>(W.C, tag, voff, (int)(base_slot * 8), true, v, first);
-  unpack8(v[0], v[1], xa);
-  unpack8(v[2], v[3], xb);
-  return sumsq16(xa, xb);
+  // wave c polls quarter c (slots [128 c, +128): lane -> values 256 c + 4 lane .. +4) into the
+  // workgroup's vector; after the four-wave barrier every wave reads its lanes' 16 values
+  Shared* S = W.C.S;
+  const int lane = W.lane, p = W.nsync & 1;
+  const int voff[1] = {16 * lane};
+  v4u v[1];
+  poll<1>(W.C, tag, voff, (int)((base_slot + 128 * W.c) * 8), true, v, first);
+  const float a = lo_h(v[0].x), b = hi_h(v[0].x), cc = lo_h(v[0].z), d = hi_h(v[0].z);
+  *(float4*)(S->xs + 256 * W.c + 4 * lane) = make_float4(a, b, cc, d);
+  const float q = wave_sum(a * a + b * b + cc * cc + d * d);
+  if (lane == 0) S->xss[p][W.c] = q;
+  sync4(W);
+  const float4 p0 = *(const float4*)(S->xs + 8 * lane), p1 = *(const float4*)(S->xs + 8 * lane + 4);
+  const float4 q0 = *(const float4*)(S->xs + 512 + 8 * lane), q1 = *(const float4*)(S->xs + 512 + 8 * lane + 4);
+  xa[0] = p0.x; xa[1] = p0.y; xa[2] = p0.z; xa[3] = p0.w; xa[4] = p1.x; xa[5] = p1.y; xa[6] = p1.z; xa[7] = p1.w;
+  xb[0] = q0.x; xb[1] = q0.y; xb[2] = q0.z; xb[3] = q0.w; xb[4] = q1.x; xb[5] = q1.y; xb[6] = q1.z; xb[7] = q1.w;
+  return (S->xss[p][0] + S->xss[p][1]) + (S->xss[p][2] + S->xss[p][3]);
 }
 // the same from a 1024-value fp16 vector in global memory (embedding row, MLP input)
 __device__ __forceinline__ float load_x1024(const _Float16* src, int lane, float (&xa)[8], float (&xb)[8]) {
@@ -567,11 +583,10 @@ __device__ __forceinline__ float load_x1024(const _Float16* src, int lane, float
     xa[e] = (float)p[e];
     xb[e] = (float)q[e];
   }
-  return sumsq16(xa, xb);
+  return wave_sum(sumsq16(xa, xb));
 }
-__device__ __forceinline__ float rstd_of(float lane_ss) {
-  return rsqrtf(wave_sum(lane_ss) * (1.0f / HIDDEN) + RMS_EPS);
-}
+// 1 / RMS of a 1024-value vector from its sum of squares
+__device__ __forceinline__ float rstd_of(float ss) { return rsqrtf(ss * (1.0f / HIDDEN) + RMS_EPS); }
 
 // the lane's 16 normalised activations a = x[8 l .. 8 l + 8), b = x[512 + 8 l ..]
 __device__ __forceinline__ void norm_act(const float (&xa)[8], const float (&xb)[8], float rstd, const h8& w0,
@@ -641,16 +656,19 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   W.gl += LINES_ATTMISC + 2 * nk;
   // the group's 512 q0 | q1 | k | v values: this lane's q values [4 lane, +4) and k | v values [256 + 4 lane, +4)
   float4 qv, kv;
-  {
-    const int voff[2] = {16 * lane, 1024 + 16 * lane};
-    v4u v[2];
-    poll<2>(W.C, tag_of(epoch, l, S_QKV), voff, (int)(xbuf(par, W.x, B_QKV) * 8), true, v,
+  {  // wave c polls slots [64 c, +64) (lanes < 32: values 128 c + 4 lane .. +4) into S->xs
+    const int voff[1] = {16 * lane};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, S_QKV), voff, (int)((xbuf(par, W.x, B_QKV) + 64 * W.c) * 8), lane < 32, v,
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
     });
-    qv = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
-    kv = make_float4(lo_h(v[1].x), hi_h(v[1].x), lo_h(v[1].z), hi_h(v[1].z));
+    if (lane < 32)
+      *(float4*)(S->xs + 128 * W.c + 4 * lane) = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
+    sync4(W);
+    qv = *(const float4*)(S->xs + 4 * lane);
+    kv = *(const float4*)(S->xs + 256 + 4 * lane);
   }
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
   const u32 nkl = n0 + LINES_ATTMISC;  // first K line
@@ -974,23 +992,26 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   W.gl += LINES_DOWN;
   float a[8];
   {
-    // slots [4 lane, 4 lane + 4) = workgroup lane / 2, waves 2 (lane % 2), +1: inter values
-    // [6 lane, 6 lane + 6) (each wave's second slot carries one value and padding);
-    // reshuffled through the wave's scratch so lanes 0-47 hold [8 lane, 8 lane + 8)
-    const int voff[2] = {32 * lane, 32 * lane + 16};
-    v4u v[2];
-    poll<2>(W.C, tag_of(epoch, l, S_GU), voff, (int)(xbuf(par, W.x, B_INT) * 8), true, v,
+    // wave c polls slot pairs k = 32 c + lane (lanes < 32): workgroup k / 4, wave k % 4 ->
+    // inter values 12 (k / 4) + 3 (k % 4) + {0, 1, 2} (the pair's last half is padding),
+    // gathered in S->xs; lanes 0-47 then own inter values [8 lane, 8 lane + 8)
+    const int voff[1] = {16 * lane};
+    v4u v[1];
+    poll<1>(W.C, tag_of(epoch, l, S_GU), voff, (int)((xbuf(par, W.x, B_INT) + 64 * W.c) * 8), lane < 32, v,
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
     });
-    float* d = S->wbuf[W.c];
-    *(float2*)(d + 6 * lane) = make_float2(lo_h(v[0].x), hi_h(v[0].x));
-    *(float2*)(d + 6 * lane + 2) = make_float2(lo_h(v[0].z), lo_h(v[1].x));
-    *(float2*)(d + 6 * lane + 4) = make_float2(hi_h(v[1].x), lo_h(v[1].z));
+    if (lane < 32) {
+      const int k = 32 * W.c + lane;
+      float* dst = S->xs + GU_PER_WG * (k >> 2) + 3 * (k & 3);
+      dst[0] = lo_h(v[0].x);
+      dst[1] = hi_h(v[0].x);
+      dst[2] = lo_h(v[0].z);
+    }
+    sync4(W);
     const int o = lane < 48 ? 8 * lane : 0;
-    asm volatile("" ::: "memory");  // reads of other lanes' writes, through another vector type
-    const float4 a0 = *(const float4*)(d + o), a1 = *(const float4*)(d + o + 4);
+    const float4 a0 = *(const float4*)(S->xs + o), a1 = *(const float4*)(S->xs + o + 4);
     const float z = lane < 48 ? 1.f : 0.f;  // lanes 48-63 contribute nothing
     a[0] = a0.x * z; a[1] = a0.y * z; a[2] = a0.z * z; a[3] = a0.w * z;
     a[4] = a1.x * z; a[5] = a1.y * z; a[6] = a1.z * z; a[7] = a1.w * z;
