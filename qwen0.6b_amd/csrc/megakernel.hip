@@ -372,7 +372,7 @@ __device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int 
       C.ok = false;
       return;
     }
-    __builtin_amdgcn_s_sleep(1);
+
   }
 }
 
@@ -390,7 +390,7 @@ __device__ __forceinline__ void lds_wait_ge(Ctl& C, const u32* p, u32 v) {
       C.ok = false;
       return;
     }
-    __builtin_amdgcn_s_sleep(1);
+
   }
   lds_acquire();
 }
@@ -524,7 +524,7 @@ __device__ __forceinline__ void wait_lines(CW& W, u32 end) {
       W.C.ok = false;
       return;
     }
-    __builtin_amdgcn_s_sleep(1);
+
   }
   lds_acquire();
 }
