@@ -586,7 +586,10 @@ __device__ __forceinline__ float load_x1024(const _Float16* src, int lane, float
   return wave_sum(sumsq16(xa, xb));
 }
 // 1 / RMS of a 1024-value vector from its sum of squares
-__device__ __forceinline__ float rstd_of(float ss) { return rsqrtf(ss * (1.0f / HIDDEN) + RMS_EPS); }
+// v_rsq_f32 for an argument >= RMS_EPS: rsqrtf adds a denormal-input path that such an
+// argument never takes (same result, six instructions fewer)
+__device__ __forceinline__ float rsq_normal(float v) { return __builtin_amdgcn_rsqf(v); }
+__device__ __forceinline__ float rstd_of(float ss) { return rsq_normal(ss * (1.0f / HIDDEN) + RMS_EPS); }
 
 // the lane's 16 normalised activations a = x[8 l .. 8 l + 8), b = x[512 + 8 l ..]
 __device__ __forceinline__ void norm_act(const float (&xa)[8], const float (&xb)[8], float rstd, const h8& w0,
@@ -681,8 +684,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     const h4 sv = *(const h4*)(misc + 768 + 2 * d4);
     const float q[4] = {qv.x, qv.y, qv.z, qv.w};
     const float k[4] = {kv.x, kv.y, kv.z, kv.w};
-    const float rq = rsqrtf(half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]) * (1.0f / HD) + RMS_EPS);
-    const float rk = rsqrtf(half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]) * (1.0f / HD) + RMS_EPS);
+    const float rq = rsq_normal(half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]) * (1.0f / HD) + RMS_EPS);
+    const float rk = rsq_normal(half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]) * (1.0f / HD) + RMS_EPS);
     float qq[4], kk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -726,23 +729,30 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       S->ring[(nkl + nk + mp) % RING_LINES][lane] = *(const v4u*)(qr + 384 + 8 * q16);
     }
   }
-  float sc[4][2];
+  // all 8 K and V line reads are issued together: a wave whose lines run past the split's
+  // last (m >= nk) reads that last line again (or, for an empty split, the misc line),
+  // which holds finite values; those positions are masked out of the softmax
+  v4u kw[4], vw[4];
   bool valid[4];
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
     const int m = 4 * W.c + bb;
+    const int mm = nk > 0 ? min(m, nk - 1) : -LINES_ATTMISC;
     valid[bb] = m < nk && t0 + 4 * m + j < t1;
-    float s0 = 0.f, s1 = 0.f;
-    if (m < nk) {
-      const v4u kw = ring_line(S, nkl + m)[lane];
-      s0 = dot8h(kw, qa);
-      s1 = dot8h(kw, qb);
-    }
-    s0 = row16_sum(s0) * P.attn_scale;
-    s1 = row16_sum(s1) * P.attn_scale;
+    kw[bb] = ring_line(S, nkl + mm)[lane];
+    vw[bb] = ring_line(S, nkl + (nk > 0 ? nk : 0) + mm)[lane];
+  }
+  float sc[4][2];
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) {
+    const float s0 = row16_sum(dot8h(kw[bb], qa)) * P.attn_scale;
+    const float s1 = row16_sum(dot8h(kw[bb], qb)) * P.attn_scale;
     sc[bb][0] = valid[bb] ? s0 : -INFINITY;
     sc[bb][1] = valid[bb] ? s1 : -INFINITY;
   }
+  // the V lines are needed here at the latest: keeps their reads in the batch above
+#pragma unroll
+  for (int bb = 0; bb < 4; ++bb) asm volatile("" ::"v"(vw[bb]));
   float mh[2], lh[2], acc[2][8];
   float pr[2][4];
 #pragma unroll
@@ -761,14 +771,11 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   }
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
-    const int m = 4 * W.c + bb;
-    if (m < nk) {
-      const h8 vh = __builtin_bit_cast(h8, ring_line(S, nkl + nk + m)[lane]);
+    const h8 vh = __builtin_bit_cast(h8, vw[bb]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        acc[0][e] = fmaf(pr[0][bb], (float)vh[e], acc[0][e]);
-        acc[1][e] = fmaf(pr[1][bb], (float)vh[e], acc[1][e]);
-      }
+    for (int e = 0; e < 8; ++e) {
+      acc[0][e] = fmaf(pr[0][bb], (float)vh[e], acc[0][e]);
+      acc[1][e] = fmaf(pr[1][bb], (float)vh[e], acc[1][e]);
     }
   }
   // sums over the 4 rows (positions) of the 16 accumulators, transposed: row R ends up
