@@ -371,15 +371,14 @@ int main() {
   {
     std::vector<int> seen(VOCAB, 0);
     CHECK(lm_row0(NWG - 1) + lm_rows(NWG - 1) == VOCAB, "lm rows end");
-    CHECK(LM_ITERS % 2 == 0, "two-buffer lm loop needs an even iteration count");
     for (int w = 0; w < NWG; ++w) {
       CHECK(lm_rows(w) <= LM_MAX_ROWS, "lm rows");
-      for (int v = 0; v < NCW + NLW; ++v)
-        for (int k = 0; k < LM_ITERS; ++k)
-          for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) {
-            const int lr = lm_local_row(v, k, j);
-            if (lr < lm_rows(w)) seen[lm_row0(w) + lr]++;
-          }
+      for (int ch = 0; ch < lm_chunks(w); ++ch)
+        for (int j = 0; j < LM_CHUNK; ++j) {
+          const int lr = lm_chunk_row(ch, j);
+          if (lr < lm_rows(w)) seen[lm_row0(w) + lr]++;
+        }
+      CHECK(lm_chunk_row(lm_chunks(w) - 1, 0) < lm_rows(w), "last chunk has a row");
     }
     for (int r = 0; r < VOCAB; ++r) CHECK(seen[r] == 1, "lm row %d seen %d", r, seen[r]);
     // ARG: workgroup w stores slots 2w, 2w + 1; quarter c polls pairs 64 c + lane

@@ -302,6 +302,7 @@ struct Shared {
   u32 cons[NCW];                   // compute wave c: ring lines below this are no longer read
   u32 xfin_cnt;                    // quarters of xfin stored (monotonic)
   u32 lm_cnt;                      // lm_head partials stored (monotonic)
+  u32 lm_next[2];                  // next lm_head chunk of the workgroup (by phase parity)
   u32 abort;
   // the layer pointer table, copied from global memory at start: reading it from
   // LDS keeps the loader waves' vmcnt free of anything but their own DMAs
@@ -416,11 +417,11 @@ __device__ __forceinline__ const v4u* ring_line(Shared* S, u32 n) { return S->ri
 // lm_head rows (every wave): rows [lm_row0(w), +lm_rows(w)) of the tied embedding,
 // 8 rows per wave per iteration, register double-buffered, dotted with xfin (fp32)
 
-__device__ __forceinline__ void lm_issue(const KParams& P, int v, int k, int r0, int nr, v4u (&buf)[16]) {
+__device__ __forceinline__ void lm_issue(const KParams& P, int ch, int r0, int nr, v4u (&buf)[16]) {
   const int lane = __lane_id();
 #pragma unroll
-  for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) {
-    int lr = lm_local_row(v, k, j);
+  for (int j = 0; j < LM_CHUNK; ++j) {
+    int lr = lm_chunk_row(ch, j);
     if (lr >= nr) lr = nr - 1;  // clamped rows are loaded but not used
     const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
     buf[2 * j] = ld_nt(base + 8 * lane);
@@ -428,12 +429,12 @@ __device__ __forceinline__ void lm_issue(const KParams& P, int v, int k, int r0,
   }
 }
 
-__device__ __forceinline__ void lm_consume(const KParams& P, int v, int k, int r0, int nr, int t, const v4u (&buf)[16],
+__device__ __forceinline__ void lm_consume(const KParams& P, int ch, int r0, int nr, int t, const v4u (&buf)[16],
                                            const float (&a)[8], const float (&b)[8], float& best, int& bidx) {
   const int lane = __lane_id();
   float part[8];
 #pragma unroll
-  for (int j = 0; j < LM_ROWS_PER_WAVE; ++j) part[j] = dot8(buf[2 * j], a) + dot8(buf[2 * j + 1], b);
+  for (int j = 0; j < LM_CHUNK; ++j) part[j] = dot8(buf[2 * j], a) + dot8(buf[2 * j + 1], b);
   float y0, y1;
   reduce8(part, y0, y1);
   // lanes 0, 16, 32, 48 hold rows (0, 4), (2, 6), (1, 5), (3, 7): each lane's rows ascend
@@ -442,7 +443,7 @@ __device__ __forceinline__ void lm_consume(const KParams& P, int v, int k, int r
     const int jr = reduce8_row(lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int lr = lm_local_row(v, k, jr + 4 * h);
+      const int lr = lm_chunk_row(ch, jr + 4 * h);
       const float val = h == 0 ? y0 : y1;
       if (lr < nr) {
         if (P.logits_out) P.logits_out[(long)t * VOCAB + r0 + lr] = val;
@@ -456,12 +457,23 @@ __device__ __forceinline__ void lm_consume(const KParams& P, int v, int k, int r
   }
 }
 
+// next chunk of this phase's shared counter (lane 0 takes it, every lane gets it)
+__device__ __forceinline__ int lm_grab(Shared* S, u32 phase) {
+  u32 ch = 0;
+  if (__lane_id() == 0) ch = __hip_atomic_fetch_add(&S->lm_next[phase & 1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return (int)__builtin_amdgcn_readfirstlane(ch);
+}
+
 __device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, u32 phase) {
   Shared* S = C.S;
   const int w = blockIdx.x, lane = __lane_id();
-  const int r0 = lm_row0(w), nr = lm_rows(w);
+  const int r0 = lm_row0(w), nr = lm_rows(w), nch = lm_chunks(w);
+  // the next phase's counter is idle until every wave has passed this phase's xfin
+  // wait, and each wave reaches that wait only after its last grab of the previous phase
+  if (v == 0 && lane == 0) lds_st(&S->lm_next[(phase + 1) & 1], 0u);
   v4u A[16], B[16];
-  lm_issue(P, v, 0, r0, nr, A);
+  int ca = lm_grab(S, phase);
+  if (ca < nch) lm_issue(P, ca, r0, nr, A);
   lds_wait_ge(C, &S->xfin_cnt, NCW * phase);
   float a[8], b[8];
   {
@@ -472,11 +484,19 @@ __device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, 
   }
   float best = -INFINITY;
   int bidx = 0x7fffffff;
-  for (int k = 0; k < LM_ITERS; k += 2) {
-    lm_issue(P, v, k + 1, r0, nr, B);
-    lm_consume(P, v, k, r0, nr, t, A, a, b, best, bidx);
-    if (k + 2 < LM_ITERS) lm_issue(P, v, k + 2, r0, nr, A);
-    lm_consume(P, v, k + 1, r0, nr, t, B, a, b, best, bidx);
+  // two chunks in flight (A, B); the older one is consumed first, and since grabs ascend,
+  // the first chunk id past the end means every later one is too
+  int cb = lm_grab(S, phase);
+  if (cb < nch) lm_issue(P, cb, r0, nr, B);
+  for (;;) {
+    if (ca >= nch) break;
+    lm_consume(P, ca, r0, nr, t, A, a, b, best, bidx);
+    ca = lm_grab(S, phase);
+    if (ca < nch) lm_issue(P, ca, r0, nr, A);
+    if (cb >= nch) break;
+    lm_consume(P, cb, r0, nr, t, B, a, b, best, bidx);
+    cb = lm_grab(S, phase);
+    if (cb < nch) lm_issue(P, cb, r0, nr, B);
   }
   wave_argmax(best, bidx);
   if (lane == 0) {
@@ -1292,6 +1312,8 @@ __global__ void __launch_bounds__(BLOCK, 1) qwen_decode_kernel(KParams P) {
     S.sync = 0;
     S.xfin_cnt = 0;
     S.lm_cnt = 0;
+    S.lm_next[0] = 0;
+    S.lm_next[1] = 0;
     S.abort = 0;
   }
   if (threadIdx.x < NLW) S.done_upto[threadIdx.x] = threadIdx.x;

@@ -196,13 +196,14 @@ QL_HD StreamGeom stream_geom(int si, int x, int i, int ctx, int pos, int lane) {
 constexpr int LM_BASE = VOCAB / NWG;        // 593
 constexpr int LM_EXTRA = VOCAB % NWG;       // 128
 constexpr int LM_MAX_ROWS = LM_BASE + 1;    // 594
-constexpr int LM_ROWS_PER_WAVE = 8;         // per iteration
-constexpr int LM_ROWS_PER_ITER = LM_ROWS_PER_WAVE * (NCW + NLW);  // 64
-constexpr int LM_ITERS = (LM_MAX_ROWS + LM_ROWS_PER_ITER - 1) / LM_ROWS_PER_ITER;  // 10 (even: two register buffers)
+constexpr int LM_CHUNK = 8;                  // rows a wave takes per grab
 QL_HD int lm_row0(int w) { return LM_BASE * w + (w < LM_EXTRA ? w : LM_EXTRA); }
 QL_HD int lm_rows(int w) { return LM_BASE + (w < LM_EXTRA ? 1 : 0); }
-// local lm_head row of wave v (0..7), iteration k, slot j (may be >= lm_rows)
-QL_HD int lm_local_row(int v, int k, int j) { return LM_ROWS_PER_ITER * k + LM_ROWS_PER_WAVE * v + j; }
+// the workgroup's rows in chunks of LM_CHUNK; its 8 waves take chunks 0, 1, 2, .. in turn
+// from a shared counter, so each wave's rows ascend
+QL_HD int lm_chunks(int w) { return (lm_rows(w) + LM_CHUNK - 1) / LM_CHUNK; }
+// local lm_head row of chunk ch, slot j (may be >= lm_rows: loaded clamped, never used)
+QL_HD int lm_chunk_row(int ch, int j) { return LM_CHUNK * ch + j; }
 
 // ---- exchange ("LL") buffers ---------------------------------------------------------
 // A slot is 8 bytes: 32 bits of payload + a 32-bit tag, written with one 8-byte
