@@ -670,15 +670,17 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   Shared* S = W.C.S;
   const int lane = W.lane, par = l & 1;
   const int pos = P.start_pos + t, ctx = pos + 1;
-  const int d4 = 4 * (lane & 31);
   _Float16* qr = (_Float16*)S->wbuf[W.c];  // roped q0 | q1 | k | v of the current position (fp16)
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_POLL);
   // ring: line n0 = q_norm | k_norm | cos[pos] | sin[pos]; K lines n0 + 1 + m; V lines n0 + 1 + nk + m
   const int t0 = att_t0(ctx, W.i), t1 = att_t1(ctx, W.i), nk = att_nk(ctx, W.i);
   const u32 n0 = W.gl;
   W.gl += LINES_ATTMISC + 2 * nk;
-  // the group's 512 q0 | q1 | k | v values: this lane's q values [4 lane, +4) and k | v values [256 + 4 lane, +4)
-  float4 qv, kv;
+  // the group's 512 q0 | q1 | k | v values: lane l (h = l / 32, dm = 2 (l % 32)) takes dims
+  // dm, dm + 1 and their rotate-half partners 64 + dm, 65 + dm of q head h, and of k (h = 0)
+  // or v (h = 1), so RoPE needs no other lane
+  const int dm = 2 * (lane & 31), hb = 128 * (lane >> 5) + dm;
+  float2 qlo, qhi, klo, khi;
   {  // wave c polls slots [64 c, +64) (lanes < 32: values 128 c + 4 lane .. +4) into S->xs
     const int voff[1] = {16 * lane};
     v4u v[1];
@@ -690,48 +692,54 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     if (lane < 32)
       *(float4*)(S->xs + 128 * W.c + 4 * lane) = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
     sync4(W);
-    qv = *(const float4*)(S->xs + 4 * lane);
-    kv = *(const float4*)(S->xs + 256 + 4 * lane);
+    qlo = *(const float2*)(S->xs + hb);
+    qhi = *(const float2*)(S->xs + hb + 64);
+    klo = *(const float2*)(S->xs + 256 + hb);
+    khi = *(const float2*)(S->xs + 256 + hb + 64);
   }
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
   const u32 nkl = n0 + LINES_ATTMISC;  // first K line
   // every wave computes the normed, roped q0 | q1 | k and v into its own scratch
   {
     const char* misc = (const char*)ring_line(S, n0);
-    const h4 qn = *(const h4*)(misc + 2 * d4);
-    const h4 kn = *(const h4*)(misc + 256 + 2 * d4);
-    const h4 cv = *(const h4*)(misc + 512 + 2 * d4);
-    const h4 sv = *(const h4*)(misc + 768 + 2 * d4);
-    const float q[4] = {qv.x, qv.y, qv.z, qv.w};
-    const float k[4] = {kv.x, kv.y, kv.z, kv.w};
+    const h2 qn0 = *(const h2*)(misc + 2 * dm), qn1 = *(const h2*)(misc + 2 * (64 + dm));
+    const h2 kn0 = *(const h2*)(misc + 256 + 2 * dm), kn1 = *(const h2*)(misc + 256 + 2 * (64 + dm));
+    const h2 cv0 = *(const h2*)(misc + 512 + 2 * dm), cv1 = *(const h2*)(misc + 512 + 2 * (64 + dm));
+    const h2 sv0 = *(const h2*)(misc + 768 + 2 * dm), sv1 = *(const h2*)(misc + 768 + 2 * (64 + dm));
+    const float qn[4] = {(float)qn0[0], (float)qn0[1], (float)qn1[0], (float)qn1[1]};
+    const float kn[4] = {(float)kn0[0], (float)kn0[1], (float)kn1[0], (float)kn1[1]};
+    const float cs[4] = {(float)cv0[0], (float)cv0[1], (float)cv1[0], (float)cv1[1]};
+    const float sn[4] = {-(float)sv0[0], -(float)sv0[1], (float)sv1[0], (float)sv1[1]};
+    const float q[4] = {qlo.x, qlo.y, qhi.x, qhi.y};
+    const float k[4] = {klo.x, klo.y, khi.x, khi.y};
     const float rq = rsq_normal(half_sum(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]) * (1.0f / HD) + RMS_EPS);
     const float rk = rsq_normal(half_sum(k[0] * k[0] + k[1] * k[1] + k[2] * k[2] + k[3] * k[3]) * (1.0f / HD) + RMS_EPS);
     float qq[4], kk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      qq[j] = q[j] * rq * (float)qn[j];
-      kk[j] = k[j] * rk * (float)kn[j];
+      qq[j] = q[j] * rq * qn[j];
+      kk[j] = k[j] * rk * kn[j];
     }
-    // rotate-half RoPE: partner dims d +- 64 live in lane ^ 16
-    const bool lo_half = (lane & 31) < 16;
+    // rotate-half RoPE: out[d] = x[d] cos[d] - x[d + 64] sin[d], out[d + 64] = x[d + 64] cos[d + 64] + x[d] sin[d + 64]
     float qo[4], ko[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float qp = xor16(qq[j]), kp = xor16(kk[j]);
-      const float cs = (float)cv[j], sn = lo_half ? -(float)sv[j] : (float)sv[j];
-      qo[j] = qq[j] * cs + qp * sn;
-      ko[j] = kk[j] * cs + kp * sn;
+      qo[j] = qq[j] * cs[j] + qq[j ^ 2] * sn[j];
+      ko[j] = kk[j] * cs[j] + kk[j ^ 2] * sn[j];
     }
     // fp16, as the values the cache keeps (and as the reference rounds q)
-    const h4 qh = {(_Float16)qo[0], (_Float16)qo[1], (_Float16)qo[2], (_Float16)qo[3]};
-    const h4 kvh = lane < 32 ? h4{(_Float16)ko[0], (_Float16)ko[1], (_Float16)ko[2], (_Float16)ko[3]}
-                             : h4{(_Float16)k[0], (_Float16)k[1], (_Float16)k[2], (_Float16)k[3]};
-    *(h4*)(qr + 4 * lane) = qh;
-    *(h4*)(qr + 256 + 4 * lane) = kvh;
+    const h2 qh0 = {(_Float16)qo[0], (_Float16)qo[1]}, qh1 = {(_Float16)qo[2], (_Float16)qo[3]};
+    const h2 kv0 = lane < 32 ? h2{(_Float16)ko[0], (_Float16)ko[1]} : h2{(_Float16)k[0], (_Float16)k[1]};
+    const h2 kv1 = lane < 32 ? h2{(_Float16)ko[2], (_Float16)ko[3]} : h2{(_Float16)k[2], (_Float16)k[3]};
+    *(h2*)(qr + hb) = qh0;
+    *(h2*)(qr + hb + 64) = qh1;
+    *(h2*)(qr + 256 + hb) = kv0;
+    *(h2*)(qr + 256 + hb + 64) = kv1;
     // the split holding `pos` writes this position's K (roped) and V to the cache
     if (W.c == 0 && att_t0(ctx, W.i) <= pos && pos < att_t1(ctx, W.i)) {
-      const long row = (((long)l * NKV + W.x) * P.max_seq + pos) * HD + d4;
-      *(h4*)((lane < 32 ? P.k_cache : P.v_cache) + row) = kvh;
+      _Float16* row = (lane < 32 ? P.k_cache : P.v_cache) + (((long)l * NKV + W.x) * P.max_seq + pos) * HD + dm;
+      *(h2*)row = kv0;
+      *(h2*)(row + 64) = kv1;
     }
   }
   // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..
