@@ -105,7 +105,7 @@ __device__ __forceinline__ v4u ld_nt(const void* p) { return __builtin_nontempor
 // 8 fp16 weights (one 16-byte load) dotted with 8 fp32 activations
 __device__ __forceinline__ float dot8(v4u w, const float (&a)[8]) {
   h8 h = __builtin_bit_cast(h8, w);
-  float s = (float)h[0] * a[0];
+  float s = fmaf((float)h[0], a[0], 0.0f);  // one v_fma_mix (see gain_act)
   s = fmaf((float)h[1], a[1], s);
   s = fmaf((float)h[2], a[2], s);
   s = fmaf((float)h[3], a[3], s);
@@ -621,6 +621,19 @@ __device__ __forceinline__ void norm_act(const float (&xa)[8], const float (&xb)
   }
 }
 
+// the lane's 16 gain-weighted activations a = x[8 l ..] * g, b = x[512 + 8 l ..] * g; the
+// RMSNorm scale rstd is applied to the row sums instead. Written as fma(x, g, +0), one
+// v_fma_mix_f32 per value (a plain product costs a conversion and a multiply); it differs
+// from x * g only in the sign of an exact zero, which no dot product sees
+__device__ __forceinline__ void gain_act(const float (&xa)[8], const float (&xb)[8], const h8& w0, const h8& w1,
+                                         float (&a)[8], float (&b)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    a[e] = fmaf(xa[e], (float)w0[e], 0.0f);
+    b[e] = fmaf(xb[e], (float)w1[e], 0.0f);
+  }
+}
+
 // one 2 KB weight row held in ring lines n, n + 1 dotted with (a | b)
 __device__ __forceinline__ float row2k(Shared* S, u32 n, int lane, const float (&a)[8], const float (&b)[8]) {
   return dot8(ring_line(S, n)[lane], a) + dot8(ring_line(S, n + 1)[lane], b);
@@ -649,14 +662,14 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   }
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
   float a[8], b[8];
-  norm_act(xa, xb, rstd_of(ss), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
-           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b);
+  gain_act(xa, xb, __builtin_bit_cast(h8, ring_line(S, n0)[lane]), __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a,
+           b);
   float part[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + LINES_NORM + 2 * (4 * W.c + r), lane, a, b);
   release_lines(W, W.gl);
   // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
-  const float rs = reduce4(part[0], part[1], part[2], part[3]);
+  const float rs = reduce4(part[0], part[1], part[2], part[3]) * rstd_of(ss);
   const float r0 = bcast(rs, 0), r1 = bcast(rs, 32), r2 = bcast(rs, 16), r3 = bcast(rs, 48);
   if (lane < 2)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_QKV) + (QKV_PER_WG / 2) * W.i + 2 * W.c + lane,
@@ -896,7 +909,7 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   trace_ev(P, t, NSTAGE * l + S_O, TR_POLL);
   const u32 n0 = W.gl;
   W.gl += LINES_O;
-  float a[8];  // attention output values [8 (lane % 32), +8)
+  v4u a;  // attention output values [8 (lane % 32), +8), fp16 as exchanged
   {
     const int voff[2] = {32 * (lane & 31), 32 * (lane & 31) + 16};
     v4u v[2];
@@ -905,13 +918,13 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
     });
-    unpack8(v[0], v[1], a);
+    a = v4u{v[0].x, v[0].z, v[1].x, v[1].z};
   }
   trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
   // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
   float part[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) part[m] = dot8(ring_line(S, n0 + 4 * W.c + m)[lane], a);
+  for (int m = 0; m < 4; ++m) part[m] = dot8h(ring_line(S, n0 + 4 * W.c + m)[lane], a);
   release_lines(W, W.gl);
   // y0 rows: (line 0 lo, line 1 lo, line 0 hi, line 1 hi) = rows 8c + (0, 2, 1, 3); y1 = +4
   const float y0 = row16_sum(pack16(part[0], part[1])), y1 = row16_sum(pack16(part[2], part[3]));
@@ -994,8 +1007,8 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   }
   trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
   float a[8], b[8];
-  norm_act(xa, xb, rstd_of(ss), __builtin_bit_cast(h8, ring_line(S, n0)[lane]),
-           __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a, b);
+  gain_act(xa, xb, __builtin_bit_cast(h8, ring_line(S, n0)[lane]), __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a,
+           b);
   const u32 ng = n0 + LINES_NORM;
   float part[6];
 #pragma unroll
@@ -1006,11 +1019,15 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   release_lines(W, W.gl);
   float pq, qq;
   reduce6(part, pq, qq);  // pq rows: gate0, gate1, up0, up1; qq rows: gate2, gate2, up2, up2
+  const float rstd = rstd_of(ss);
+  pq *= rstd;
+  qq *= rstd;
   const float g0 = bcast(pq, 0), g1 = bcast(pq, 16), u0 = bcast(pq, 32), u1 = bcast(pq, 48);
   const float g2 = bcast(qq, 0), u2 = bcast(qq, 32);
-  const float s0 = g0 / (1.0f + __expf(-g0)) * u0;
-  const float s1 = g1 / (1.0f + __expf(-g1)) * u1;
-  const float s2 = g2 / (1.0f + __expf(-g2)) * u2;
+  // SiLU(g) * u with v_rcp_f32 (1 ulp) in place of an IEEE divide
+  const float s0 = g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)) * u0;
+  const float s1 = g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1)) * u1;
+  const float s2 = g2 * __builtin_amdgcn_rcpf(1.0f + __expf(-g2)) * u2;
   if (lane < 2)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_INT) + int_slot(W.i, W.c, lane), lane == 0 ? pack_h2(s0, s1) : pack_h2(s2, 0.f),
              tag_of(epoch, l, S_GU));
@@ -1025,7 +1042,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_POLL);
   const u32 n0 = W.gl;
   W.gl += LINES_DOWN;
-  float a[8];
+  v4u a;
   {
     // wave c polls slot pairs k = 32 c + lane (lanes < 32): workgroup k / 4, wave k % 4 ->
     // inter values 12 (k / 4) + 3 (k % 4) + {0, 1, 2} (the pair's last half is padding),
@@ -1047,14 +1064,15 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
     sync4(W);
     const int o = lane < 48 ? 8 * lane : 0;
     const float4 a0 = *(const float4*)(S->xs + o), a1 = *(const float4*)(S->xs + o + 4);
-    const float z = lane < 48 ? 1.f : 0.f;  // lanes 48-63 contribute nothing
-    a[0] = a0.x * z; a[1] = a0.y * z; a[2] = a0.z * z; a[3] = a0.w * z;
-    a[4] = a1.x * z; a[5] = a1.y * z; a[6] = a1.z * z; a[7] = a1.w * z;
+    // back to the fp16 values they were exchanged as (exact); lanes 48-63 contribute nothing
+    const h8 ah = {(_Float16)a0.x, (_Float16)a0.y, (_Float16)a0.z, (_Float16)a0.w,
+                   (_Float16)a1.x, (_Float16)a1.y, (_Float16)a1.z, (_Float16)a1.w};
+    a = lane < 48 ? __builtin_bit_cast(v4u, ah) : v4u{0, 0, 0, 0};
   }
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
   float part[8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r) part[r] = dot8(ring_line(S, n0 + 8 * W.c + r)[lane], a);
+  for (int r = 0; r < 8; ++r) part[r] = dot8h(ring_line(S, n0 + 8 * W.c + r)[lane], a);
   release_lines(W, W.gl);
   float y0, y1;
   reduce8(part, y0, y1);
