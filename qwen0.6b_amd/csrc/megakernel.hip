@@ -142,6 +142,13 @@ __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
 constexpr int ROR8 = 0x128, ROR4 = 0x124, ROR2 = 0x122, ROR1 = 0x121;
+// max of two non-NaN values as one v_max_f32: fmaxf adds two canonicalizing ops for
+// values that come out of lane permutes (this kernel runs in IEEE mode)
+__device__ __forceinline__ float fmax2(float a, float b) {
+  float r;
+  asm("v_max_f32_e32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 // every lane: sum of its 16-lane row
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp<ROR8>(v);
@@ -151,10 +158,10 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 __device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<ROR8>(v));
-  v = fmaxf(v, dpp<ROR4>(v));
-  v = fmaxf(v, dpp<ROR2>(v));
-  v = fmaxf(v, dpp<ROR1>(v));
+  v = fmax2(v, dpp<ROR8>(v));
+  v = fmax2(v, dpp<ROR4>(v));
+  v = fmax2(v, dpp<ROR2>(v));
+  v = fmax2(v, dpp<ROR1>(v));
   return v;
 }
 // rows of the result: 0 = a.r0 + a.r1, 1 = b.r0 + b.r1, 2 = a.r2 + a.r3, 3 = b.r2 + b.r3
@@ -169,11 +176,11 @@ __device__ __forceinline__ float pack32(float a, float b) {
 }
 __device__ __forceinline__ float max16x(float v) {  // max of partner rows (0<->1, 2<->3)
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float max32x(float v) {  // max of the two 32-lane halves
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return fmax2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 // every lane: sum over the whole wave
 __device__ __forceinline__ float wave_sum(float v) { return row16_sum(pack16(pack32(v, v), pack32(v, v))); }
@@ -895,7 +902,7 @@ __device__ __forceinline__ void st_comb(CW& W, const KParams& P, int t, int l, u
   const float Lt = half_sum(e * __uint_as_float(v[0].z));
   const float oa = half_sum(e * __uint_as_float(v[1].x));
   const float ob = half_sum(e * __uint_as_float(v[1].z));
-  const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+  const float inv = Lt > 0.f ? __builtin_amdgcn_rcpf(Lt) : 0.f;  // v_rcp_f32 (1 ulp)
   if (lane == 0)
     ll_store_xcd(P.ws, xbuf(par, W.x, B_ATTO) + 4 * W.i + W.c, pack_h2(oa * inv, ob * inv), tag_of(epoch, l, S_COMB));
   drain_stores(S_COMB);
