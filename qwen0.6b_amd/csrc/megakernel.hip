@@ -324,11 +324,14 @@ struct Ctl {
   u64 deadline;
 };
 
-__device__ __forceinline__ bool give_up(Ctl& C, u64 t0, int& spins) {
+// t0 == 0: the wait's clock starts at its 16th spin (a poll's first sweeps pay no clock read)
+__device__ __forceinline__ bool give_up(Ctl& C, u64& t0, int& spins) {
   ++spins;
   if ((spins & 15) == 0) {
     if (lds_ld(&C.S->abort)) return true;
-    if (wall_clock64() - t0 > C.deadline) {
+    const u64 now = wall_clock64();
+    if (t0 == 0) t0 = now;
+    if (now - t0 > C.deadline) {
       __hip_atomic_fetch_or(C.P->status, ST_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       lds_st(&C.S->abort, 1u);
       return true;
@@ -361,7 +364,7 @@ __device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int 
     first();
     return;
   }
-  const u64 t0 = wall_clock64();
+  u64 t0 = 0;
   int spins = 0;
   for (bool once = true;; once = false) {
     asm volatile("" ::: "memory");
@@ -391,7 +394,7 @@ __device__ __forceinline__ void lds_wait_ge(Ctl& C, const u32* p, u32 v) {
     lds_acquire();
     return;
   }
-  const u64 t0 = wall_clock64();
+  u64 t0 = wall_clock64();
   int spins = 0;
   while (lds_ld(p) < v) {
     if (give_up(C, t0, spins)) {
@@ -544,7 +547,7 @@ __device__ __forceinline__ void wait_lines(CW& W, u32 end) {
     lds_acquire();
     return;
   }
-  const u64 t0 = wall_clock64();
+  u64 t0 = wall_clock64();
   int spins = 0;
   while (lines_done(W.C.S) < end) {
     if (give_up(W.C, t0, spins)) {
@@ -1299,7 +1302,7 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
                 wait_vmcnt<0>();
                 if (pending > 0) lds_st(&S->done_upto[q], last + 4);
                 pending = 0;
-                const u64 t0 = wall_clock64();
+                u64 t0 = wall_clock64();
                 int spins = 0;
                 while (n >= (avail = cons_min(S) + RING_LINES)) {
                   if (give_up(C, t0, spins)) {
