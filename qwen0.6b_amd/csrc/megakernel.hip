@@ -704,16 +704,17 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   // or v (h = 1), so RoPE needs no other lane
   const int dm = 2 * (lane & 31), hb = 128 * (lane >> 5) + dm;
   float2 qlo, qhi, klo, khi;
-  {  // wave c polls slots [64 c, +64) (lanes < 32: values 128 c + 4 lane .. +4) into S->xs
-    const int voff[1] = {16 * lane};
+  {  // wave c polls slots [64 c, +64) (lane % 32: values 128 c + 4 (lane % 32) .. +4) into S->xs;
+     // lanes 32-63 repeat lanes 0-31 (same lines, same values), which keeps the wave unbranched
+    const int voff[1] = {16 * (lane & 31)};
     v4u v[1];
-    poll<1>(W.C, tag_of(epoch, l, S_QKV), voff, (int)((xbuf(par, W.x, B_QKV) + 64 * W.c) * 8), lane < 32, v,
+    poll<1>(W.C, tag_of(epoch, l, S_QKV), voff, (int)((xbuf(par, W.x, B_QKV) + 64 * W.c) * 8), true, v,
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
     });
-    if (lane < 32)
-      *(float4*)(S->xs + 128 * W.c + 4 * lane) = make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
+    *(float4*)(S->xs + 128 * W.c + 4 * (lane & 31)) =
+        make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
     sync4(W);
     qlo = *(const float2*)(S->xs + hb);
     qhi = *(const float2*)(S->xs + hb + 64);
@@ -752,8 +753,11 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     }
     // fp16, as the values the cache keeps (and as the reference rounds q)
     const h2 qh0 = {(_Float16)qo[0], (_Float16)qo[1]}, qh1 = {(_Float16)qo[2], (_Float16)qo[3]};
-    const h2 kv0 = lane < 32 ? h2{(_Float16)ko[0], (_Float16)ko[1]} : h2{(_Float16)k[0], (_Float16)k[1]};
-    const h2 kv1 = lane < 32 ? h2{(_Float16)ko[2], (_Float16)ko[3]} : h2{(_Float16)k[2], (_Float16)k[3]};
+    // lanes 0-31 keep the normed, roped k; lanes 32-63 the raw v (selected per value, unbranched)
+    float kx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kx[j] = lane < 32 ? ko[j] : k[j];
+    const h2 kv0 = {(_Float16)kx[0], (_Float16)kx[1]}, kv1 = {(_Float16)kx[2], (_Float16)kx[3]};
     *(h2*)(qr + hb) = qh0;
     *(h2*)(qr + hb + 64) = qh1;
     *(h2*)(qr + 256 + hb) = kv0;
@@ -773,11 +777,12 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   const v4u qa = *(const v4u*)(qr + 8 * q16), qb = *(const v4u*)(qr + 128 + 8 * q16);  // q heads 0, 1 (fp16)
   // the current position is not in the cache lines (the loader reads a spare row for it):
   // the wave whose 16 positions include it writes its fp16 k and v into its own ring lines
+  // (row jp of the line; all four rows of lanes write the same 16 bytes, so no lane branches)
   {
     const int mp = (pos - t0) >> 2, jp = (pos - t0) & 3;
-    if (pos >= t0 && pos < t1 && (mp >> 2) == W.c && j == jp) {
-      S->ring[(nkl + mp) % RING_LINES][lane] = *(const v4u*)(qr + 256 + 8 * q16);
-      S->ring[(nkl + nk + mp) % RING_LINES][lane] = *(const v4u*)(qr + 384 + 8 * q16);
+    if (pos >= t0 && pos < t1 && (mp >> 2) == W.c) {
+      S->ring[(nkl + mp) % RING_LINES][16 * jp + q16] = *(const v4u*)(qr + 256 + 8 * q16);
+      S->ring[(nkl + nk + mp) % RING_LINES][16 * jp + q16] = *(const v4u*)(qr + 384 + 8 * q16);
     }
   }
   // all 8 K and V line reads are issued together: a wave whose lines run past the split's
@@ -845,44 +850,44 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     const int R = lane >> 4;
     *(float4*)(rec + (R >> 1) * PART_PER_HEAD + 2 + 8 * q16 + 4 * (R & 1)) = make_float4(u[0], u[1], u[2], u[3]);
   }
-  if (lane == 0) {
-    rec[0] = mh[0];
-    rec[1] = lh[0];
-    rec[PART_PER_HEAD] = mh[1];
-    rec[PART_PER_HEAD + 1] = lh[1];
-  }
+  // m and l are uniform over the wave: every lane writes the same values
+  *(float2*)rec = make_float2(mh[0], lh[0]);
+  *(float2*)(rec + PART_PER_HEAD) = make_float2(mh[1], lh[1]);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_SYNC);
   sync4(W);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_MERGE);
-  // merge the 4 wave partials: wave c writes entries [65 c, 65 c + 65) of the 260
-  float Mx[2], wt[2][NCW];
+  // merge the 4 wave partials: wave c writes the 64 accumulators of head c / 2, dims
+  // 64 (c % 2) + lane; wave 0 lanes 0-3 also write (M, L) of both heads
+  const int hm = W.c >> 1;
+  float wt[NCW];
+  float Mh = -INFINITY;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int cc = 0; cc < NCW; ++cc) Mh = fmaxf(Mh, S->apart[cc][hm][0]);
+#pragma unroll
+  for (int cc = 0; cc < NCW; ++cc) {
+    const float mc = S->apart[cc][hm][0];
+    wt[cc] = (mc == -INFINITY) ? 0.f : __expf(mc - Mh);
+  }
+  {
+    const int k = 2 + 64 * (W.c & 1) + lane;
+    float val = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < NCW; ++cc) val = fmaf(wt[cc], S->apart[cc][hm][k], val);
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, hm, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
+  }
+  if (W.c == 0 && lane < 4) {
+    const int h = lane >> 1;
     float M = -INFINITY;
 #pragma unroll
     for (int cc = 0; cc < NCW; ++cc) M = fmaxf(M, S->apart[cc][h][0]);
-    Mx[h] = M;
+    float L = 0.f;
 #pragma unroll
     for (int cc = 0; cc < NCW; ++cc) {
       const float mc = S->apart[cc][h][0];
-      wt[h][cc] = (mc == -INFINITY) ? 0.f : __expf(mc - M);
+      L = fmaf((mc == -INFINITY) ? 0.f : __expf(mc - M), S->apart[cc][h][1], L);
     }
-  }
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    if (it == 0 || lane == 0) {
-      const int e = 65 * W.c + (it == 0 ? lane : 64);
-      const int h = e >= PART_PER_HEAD ? 1 : 0;
-      const int k = e - PART_PER_HEAD * h;
-      float val = 0.f;
-      if (k == 0) {
-        val = Mx[h];
-      } else {
-#pragma unroll
-        for (int cc = 0; cc < NCW; ++cc) val = fmaf(h ? wt[1][cc] : wt[0][cc], S->apart[cc][h][k], val);
-      }
-      ll_store_xcd(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, k), __float_as_uint(val), tag_of(epoch, l, S_ATT));
-    }
+    ll_store_xcd(P.ws, xbuf(par, W.x, B_PART) + part_index(W.i, h, lane & 1), __float_as_uint((lane & 1) ? L : M),
+                 tag_of(epoch, l, S_ATT));
   }
   drain_stores(S_ATT);
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_STORE);
