@@ -422,6 +422,13 @@ __device__ __forceinline__ void trace_ev(const KParams& P, int token, int stage,
 }
 
 __device__ __forceinline__ const v4u* ring_line(Shared* S, u32 n) { return S->ring[n % RING_LINES]; }
+// A stage's lines from its first global line n0: vb = this lane's byte offset of line n0
+// in the ring, and line n0 + k is at (vb + 1024 k) mod the ring size (the ring is the first
+// 128 KB of LDS), one add and one and per line
+__device__ __forceinline__ u32 ring_vbase(u32 n0, int lane) { return (n0 % RING_LINES) * LINE_BYTES + 16 * lane; }
+__device__ __forceinline__ v4u ring_ld(const Shared* S, u32 vb, int k) {
+  return *(const v4u*)((const char*)S->ring + ((vb + (u32)k * LINE_BYTES) & (RING_LINES * LINE_BYTES - 1)));
+}
 
 // ------------------------------------------------------------------------------------
 // lm_head rows (every wave): rows [lm_row0(w), +lm_rows(w)) of the tied embedding,
@@ -645,8 +652,8 @@ __device__ __forceinline__ void gain_act(const float (&xa)[8], const float (&xb)
 }
 
 // one 2 KB weight row held in ring lines n, n + 1 dotted with (a | b)
-__device__ __forceinline__ float row2k(Shared* S, u32 n, int lane, const float (&a)[8], const float (&b)[8]) {
-  return dot8(ring_line(S, n)[lane], a) + dot8(ring_line(S, n + 1)[lane], b);
+__device__ __forceinline__ float row2k(const Shared* S, u32 vb, int k, const float (&a)[8], const float (&b)[8]) {
+  return dot8(ring_ld(S, vb, k), a) + dot8(ring_ld(S, vb, k + 1), b);
 }
 
 // ---- stages ----------------------------------------------------------------------------
@@ -672,11 +679,11 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   }
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
   float a[8], b[8];
-  gain_act(xa, xb, __builtin_bit_cast(h8, ring_line(S, n0)[lane]), __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a,
-           b);
+  const u32 vb = ring_vbase(n0, lane);
+  gain_act(xa, xb, __builtin_bit_cast(h8, ring_ld(S, vb, 0)), __builtin_bit_cast(h8, ring_ld(S, vb, 1)), a, b);
   float part[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) part[r] = row2k(S, n0 + LINES_NORM + 2 * (4 * W.c + r), lane, a, b);
+  for (int r = 0; r < 4; ++r) part[r] = row2k(S, vb, LINES_NORM + 2 * (4 * W.c + r), a, b);
   release_lines(W, W.gl);
   // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
   const float rs = reduce4(part[0], part[1], part[2], part[3]) * rstd_of(ss);
@@ -723,9 +730,10 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   }
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
   const u32 nkl = n0 + LINES_ATTMISC;  // first K line
+  const u32 vbk = ring_vbase(nkl, lane);
   // every wave computes the normed, roped q0 | q1 | k and v into its own scratch
   {
-    const char* misc = (const char*)ring_line(S, n0);
+    const char* misc = (const char*)S->ring[n0 % RING_LINES];
     const h2 qn0 = *(const h2*)(misc + 2 * dm), qn1 = *(const h2*)(misc + 2 * (64 + dm));
     const h2 kn0 = *(const h2*)(misc + 256 + 2 * dm), kn1 = *(const h2*)(misc + 256 + 2 * (64 + dm));
     const h2 cv0 = *(const h2*)(misc + 512 + 2 * dm), cv1 = *(const h2*)(misc + 512 + 2 * (64 + dm));
@@ -795,8 +803,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     const int m = 4 * W.c + bb;
     const int mm = nk > 0 ? min(m, nk - 1) : -LINES_ATTMISC;
     valid[bb] = m < nk && t0 + 4 * m + j < t1;
-    kw[bb] = ring_line(S, nkl + mm)[lane];
-    vw[bb] = ring_line(S, nkl + (nk > 0 ? nk : 0) + mm)[lane];
+    kw[bb] = ring_ld(S, vbk, mm);
+    vw[bb] = ring_ld(S, vbk, (nk > 0 ? nk : 0) + mm);
   }
   float sc[4][2];
 #pragma unroll
@@ -938,8 +946,9 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
   // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
   float part[4];
+  const u32 vb = ring_vbase(n0, lane);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) part[m] = dot8h(ring_line(S, n0 + 4 * W.c + m)[lane], a);
+  for (int m = 0; m < 4; ++m) part[m] = dot8h(ring_ld(S, vb, 4 * W.c + m), a);
   release_lines(W, W.gl);
   // y0 rows: (line 0 lo, line 1 lo, line 0 hi, line 1 hi) = rows 8c + (0, 2, 1, 3); y1 = +4
   const float y0 = row16_sum(pack16(part[0], part[1])), y1 = row16_sum(pack16(part[2], part[3]));
@@ -1022,14 +1031,14 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   }
   trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
   float a[8], b[8];
-  gain_act(xa, xb, __builtin_bit_cast(h8, ring_line(S, n0)[lane]), __builtin_bit_cast(h8, ring_line(S, n0 + 1)[lane]), a,
-           b);
-  const u32 ng = n0 + LINES_NORM;
+  const u32 vb = ring_vbase(n0, lane);
+  gain_act(xa, xb, __builtin_bit_cast(h8, ring_ld(S, vb, 0)), __builtin_bit_cast(h8, ring_ld(S, vb, 1)), a, b);
+  constexpr int ng = LINES_NORM;
   float part[6];
 #pragma unroll
   for (int jj = 0; jj < 3; ++jj) {
-    part[jj] = row2k(S, ng + 2 * (3 * W.c + jj), lane, a, b);                          // gate
-    part[3 + jj] = row2k(S, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj), lane, a, b);      // up
+    part[jj] = row2k(S, vb, ng + 2 * (3 * W.c + jj), a, b);                          // gate
+    part[3 + jj] = row2k(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj), a, b);      // up
   }
   release_lines(W, W.gl);
   float pq, qq;
@@ -1086,8 +1095,9 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   }
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
   float part[8];
+  const u32 vb = ring_vbase(n0, lane);
 #pragma unroll
-  for (int r = 0; r < 8; ++r) part[r] = dot8h(ring_line(S, n0 + 8 * W.c + r)[lane], a);
+  for (int r = 0; r < 8; ++r) part[r] = dot8h(ring_ld(S, vb, 8 * W.c + r), a);
   release_lines(W, W.gl);
   float y0, y1;
   reduce8(part, y0, y1);
