@@ -354,36 +354,46 @@ struct NoPre {
 template <int K, typename Pre = NoPre>
 __device__ __forceinline__ void poll(Ctl& C, u32 tag, const int (&voff)[K], int soff, bool active, v4u (&out)[K],
                                      Pre first = Pre()) {
-  bool done[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    done[k] = !active;
-    out[k] = v4u{0, 0, 0, 0};
-  }
+  for (int k = 0; k < K; ++k) out[k] = v4u{0, 0, 0, 0};
   if (!C.ok) {
     first();
     return;
   }
+  // first sweep: every active lane loads all its pairs (most polls end here)
+  asm volatile("" ::: "memory");
+  if (active) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) out[k] = ld_pair(C.r, voff[k], soff);
+  }
+  first();
+  bool done[K];
+  bool all = true;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    done[k] = !active || ((out[k].y == tag) && (out[k].w == tag));
+    all = all && done[k];
+  }
+  if (__all(all)) return;
+  // later sweeps reload only the pairs still missing
   u64 t0 = 0;
   int spins = 0;
-  for (bool once = true;; once = false) {
+  for (;;) {
+    if (give_up(C, t0, spins)) {
+      C.ok = false;
+      return;
+    }
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < K; ++k)
       if (!done[k]) out[k] = ld_pair(C.r, voff[k], soff);
-    if (once) first();
-    bool all = true;
+    all = true;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       if (!done[k]) done[k] = (out[k].y == tag) && (out[k].w == tag);
       all = all && done[k];
     }
     if (__all(all)) return;
-    if (give_up(C, t0, spins)) {
-      C.ok = false;
-      return;
-    }
-
   }
 }
 
