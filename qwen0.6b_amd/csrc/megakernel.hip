@@ -544,10 +544,13 @@ struct CW {
   u32 gl;      // global ring line index of the next stage
 };
 
-// barrier of the 4 compute waves (monotonic LDS counter)
+// LDS byte address of a workgroup-shared variable
+__device__ __forceinline__ u32 lds_addr(const void* p) { return (u32)(size_t)(const __attribute__((address_space(3))) void*)p; }
+// barrier of the 4 compute waves (monotonic LDS counter); lane 0 adds with a plain ds_add_u32
+// (the compiler's atomic optimizer would first count the active lanes)
 __device__ __forceinline__ void sync4(CW& W) {
   lds_release();
-  if (W.lane == 0) __hip_atomic_fetch_add(&W.C.S->sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (W.lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(lds_addr(&W.C.S->sync)), "v"(1u) : "memory");
   ++W.nsync;
   lds_wait_ge(W.C, &W.C.S->sync, NCW * W.nsync);
 }
