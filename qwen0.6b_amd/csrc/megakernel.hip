@@ -426,9 +426,12 @@ __device__ __forceinline__ void drain_stores(int stage) {
   if ((STORE_DRAIN_MASK >> stage) & 1) wait_vmcnt<0>();
 }
 
+// a uniform branch (one scalar compare per call site when tracing is off); lane 0 stores
 __device__ __forceinline__ void trace_ev(const KParams& P, int token, int stage, int what) {
-  if (P.trace && token == P.trace_token && __lane_id() == 0)
-    P.trace[((long)blockIdx.x * trace_stages(P.num_layers) + stage) * TRACE_EVENTS + what] = wall_clock64();
+  if (__builtin_expect(P.trace != nullptr && token == P.trace_token, 0)) {
+    const u64 now = wall_clock64();
+    if (__lane_id() == 0) P.trace[((long)blockIdx.x * trace_stages(P.num_layers) + stage) * TRACE_EVENTS + what] = now;
+  }
 }
 
 __device__ __forceinline__ const v4u* ring_line(Shared* S, u32 n) { return S->ring[n % RING_LINES]; }
