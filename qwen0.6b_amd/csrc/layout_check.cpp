@@ -370,16 +370,14 @@ int main() {
   // ---- lm_head rows: [0, VOCAB) exactly once over (w, v, k, j) ----
   {
     std::vector<int> seen(VOCAB, 0);
-    CHECK(lm_row0(NWG - 1) + lm_rows(NWG - 1) == VOCAB, "lm rows end");
-    for (int w = 0; w < NWG; ++w) {
-      CHECK(lm_rows(w) <= LM_MAX_ROWS, "lm rows");
+    for (int w = 0; w < NWG; ++w)
       for (int ch = 0; ch < lm_chunks(w); ++ch)
         for (int j = 0; j < LM_CHUNK; ++j) {
-          const int lr = lm_chunk_row(ch, j);
-          if (lr < lm_rows(w)) seen[lm_row0(w) + lr]++;
+          const int r = lm_row(w, ch, j);
+          CHECK(r >= 0 && r < VOCAB, "lm row range");
+          CHECK(ch == 0 || r > lm_row(w, ch - 1, LM_CHUNK - 1), "lm rows ascend");
+          seen[r]++;
         }
-      CHECK(lm_chunk_row(lm_chunks(w) - 1, 0) < lm_rows(w), "last chunk has a row");
-    }
     for (int r = 0; r < VOCAB; ++r) CHECK(seen[r] == 1, "lm row %d seen %d", r, seen[r]);
     // ARG: workgroup w stores slots 2w, 2w + 1; quarter c polls pairs 64 c + lane
     for (int c = 0; c < NCW; ++c)

@@ -444,22 +444,20 @@ __device__ __forceinline__ v4u ring_ld(const Shared* S, u32 vb, int k) {
 }
 
 // ------------------------------------------------------------------------------------
-// lm_head rows (every wave): rows [lm_row0(w), +lm_rows(w)) of the tied embedding,
-// 8 rows per wave per iteration, register double-buffered, dotted with xfin (fp32)
+// lm_head rows (every wave): the workgroup's 8-row chunks of the tied embedding, two
+// chunks in registers per wave, dotted with xfin (fp32)
 
-__device__ __forceinline__ void lm_issue(const KParams& P, int ch, int r0, int nr, v4u (&buf)[16]) {
+__device__ __forceinline__ void lm_issue(const KParams& P, int w, int ch, v4u (&buf)[16]) {
   const int lane = __lane_id();
 #pragma unroll
   for (int j = 0; j < LM_CHUNK; ++j) {
-    int lr = lm_chunk_row(ch, j);
-    if (lr >= nr) lr = nr - 1;  // clamped rows are loaded but not used
-    const _Float16* base = P.lm_head + (long)(r0 + lr) * HIDDEN;
+    const _Float16* base = P.lm_head + (long)lm_row(w, ch, j) * HIDDEN;
     buf[2 * j] = ld_nt(base + 8 * lane);
     buf[2 * j + 1] = ld_nt(base + 512 + 8 * lane);
   }
 }
 
-__device__ __forceinline__ void lm_consume(const KParams& P, int ch, int r0, int nr, int t, const v4u (&buf)[16],
+__device__ __forceinline__ void lm_consume(const KParams& P, int w, int ch, int t, const v4u (&buf)[16],
                                            const float (&a)[8], const float (&b)[8], float& best, int& bidx) {
   const int lane = __lane_id();
   float part[8];
@@ -473,15 +471,13 @@ __device__ __forceinline__ void lm_consume(const KParams& P, int ch, int r0, int
     const int jr = reduce8_row(lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int lr = lm_chunk_row(ch, jr + 4 * h);
+      const int row = lm_row(w, ch, jr + 4 * h);
       const float val = h == 0 ? y0 : y1;
-      if (lr < nr) {
-        if (P.logits_out) P.logits_out[(long)t * VOCAB + r0 + lr] = val;
-        const float vv = __builtin_isnan(val) ? -INFINITY : val;
-        if (vv > best) {
-          best = vv;
-          bidx = r0 + lr;
-        }
+      if (P.logits_out) P.logits_out[(long)t * VOCAB + row] = val;
+      const float vv = __builtin_isnan(val) ? -INFINITY : val;
+      if (vv > best) {
+        best = vv;
+        bidx = row;
       }
     }
   }
@@ -497,13 +493,13 @@ __device__ __forceinline__ int lm_grab(Shared* S, u32 phase) {
 __device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, u32 phase) {
   Shared* S = C.S;
   const int w = blockIdx.x, lane = __lane_id();
-  const int r0 = lm_row0(w), nr = lm_rows(w), nch = lm_chunks(w);
+  const int nch = lm_chunks(w);
   // the next phase's counter is idle until every wave has passed this phase's xfin
   // wait, and each wave reaches that wait only after its last grab of the previous phase
   if (v == 0 && lane == 0) lds_st(&S->lm_next[(phase + 1) & 1], 0u);
   v4u A[16], B[16];
   int ca = lm_grab(S, phase);
-  if (ca < nch) lm_issue(P, ca, r0, nr, A);
+  if (ca < nch) lm_issue(P, w, ca, A);
   lds_wait_ge(C, &S->xfin_cnt, NCW * phase);
   float a[8], b[8];
   {
@@ -517,16 +513,16 @@ __device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, 
   // two chunks in flight (A, B); the older one is consumed first, and since grabs ascend,
   // the first chunk id past the end means every later one is too
   int cb = lm_grab(S, phase);
-  if (cb < nch) lm_issue(P, cb, r0, nr, B);
+  if (cb < nch) lm_issue(P, w, cb, B);
   for (;;) {
     if (ca >= nch) break;
-    lm_consume(P, ca, r0, nr, t, A, a, b, best, bidx);
+    lm_consume(P, w, ca, t, A, a, b, best, bidx);
     ca = lm_grab(S, phase);
-    if (ca < nch) lm_issue(P, ca, r0, nr, A);
+    if (ca < nch) lm_issue(P, w, ca, A);
     if (cb >= nch) break;
-    lm_consume(P, cb, r0, nr, t, B, a, b, best, bidx);
+    lm_consume(P, w, cb, t, B, a, b, best, bidx);
     cb = lm_grab(S, phase);
-    if (cb < nch) lm_issue(P, cb, r0, nr, B);
+    if (cb < nch) lm_issue(P, w, cb, B);
   }
   wave_argmax(best, bidx);
   if (lane == 0) {

@@ -193,17 +193,15 @@ QL_HD StreamGeom stream_geom(int si, int x, int i, int ctx, int pos, int lane) {
 }
 
 // ---- LM head ------------------------------------------------------------------------
-constexpr int LM_BASE = VOCAB / NWG;        // 593
-constexpr int LM_EXTRA = VOCAB % NWG;       // 128
-constexpr int LM_MAX_ROWS = LM_BASE + 1;    // 594
 constexpr int LM_CHUNK = 8;                  // rows a wave takes per grab
-QL_HD int lm_row0(int w) { return LM_BASE * w + (w < LM_EXTRA ? w : LM_EXTRA); }
-QL_HD int lm_rows(int w) { return LM_BASE + (w < LM_EXTRA ? 1 : 0); }
-// the workgroup's rows in chunks of LM_CHUNK; its 8 waves take chunks 0, 1, 2, .. in turn
-// from a shared counter, so each wave's rows ascend
-QL_HD int lm_chunks(int w) { return (lm_rows(w) + LM_CHUNK - 1) / LM_CHUNK; }
-// local lm_head row of chunk ch, slot j (may be >= lm_rows: loaded clamped, never used)
-QL_HD int lm_chunk_row(int ch, int j) { return LM_CHUNK * ch + j; }
+static_assert(VOCAB % LM_CHUNK == 0, "whole chunks");
+constexpr int LM_NCHUNK = VOCAB / LM_CHUNK;  // 18992
+// The vocabulary's 8-row chunks are dealt to the workgroups in turn (chunk g to workgroup
+// g mod NWG), so every workgroup streams rows from the whole table; a workgroup's 8 waves
+// take its chunks 0, 1, 2, .. in turn from a shared counter, so each wave's rows ascend.
+QL_HD int lm_chunks(int w) { return (LM_NCHUNK - w + NWG - 1) / NWG; }
+// lm_head row of workgroup w's chunk ch, slot j
+QL_HD int lm_row(int w, int ch, int j) { return LM_CHUNK * (w + NWG * ch) + j; }
 
 // ---- exchange ("LL") buffers ---------------------------------------------------------
 // A slot is 8 bytes: 32 bits of payload + a 32-bit tag, written with one 8-byte
