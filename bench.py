@@ -90,6 +90,122 @@ def cpu_baseline(hw, budget_s=12.0, max_steps=400):
                        f"(28 layers + lm_head, random KV history), {dt:.1f} s")
 
 
+def _median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+def aux_line(metric, value, unit, higher, workload, cfg, kernel, bytes_per_call, call_ms, steps, warmup, dtype="fp16"):
+    """JSON line of an auxiliary workload (--workload other than the default)."""
+    achieved = bytes_per_call / (call_ms / 1e3) / 1e9
+    return {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(call_ms, 4), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+        "dtype": dtype, "data": "synthetic: seeded N(0,0.02) fp16 weights (norms 1.0)",
+        "config": dict(workload=workload, **cfg),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kernel,
+                     "bytes_per_launch": bytes_per_call, "kernel_ms": round(call_ms, 4)},
+        "cpu_baseline": None,
+    }
+
+
+def run_generate(args, n_prompt, n_new, name):
+    """C0 / C3: prefill an n_prompt-id prompt (all but its last id), then one generate_nosync
+    launch of n_new greedy tokens; the median launch time over --steps launches."""
+    import torch
+
+    import qwen_weights as qw
+    import Qwen06B_architecture as qa
+
+    w = qw.device_weights(qw.host_weights(seed=0, std=0.02), "cuda")
+    dec = qa.Decoder(weights=w, verbose=False)
+    prompt = qw.synthetic_prompt(n_prompt, seed=1)
+    ts = []
+    for rep in range(args.warmup + args.steps):
+        dec.reset()
+        dec.prefill(prompt[:-1])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec.generate_nosync(prompt[-1], n_new)
+        e1.record()
+        torch.cuda.synchronize()
+        if rep >= args.warmup:
+            ts.append(e0.elapsed_time(e1))
+    qa._check_device_errors()
+    ms = _median(ts)
+    start = n_prompt - 1
+    return aux_line(f"batch-1 decode tokens/sec ({name}: {n_prompt}-id prompt, generate_nosync {n_new})",
+                    round(n_new / ms * 1e3, 2), "tokens/s", True, name,
+                    {"prompt": n_prompt, "new_tokens": n_new, "positions": f"{start}..{start + n_new - 1}"},
+                    "qwen_decode_kernel", algorithmic_bytes(start, n_new), ms, args.steps, args.warmup)
+
+
+def run_lm_head(args):
+    """C1: isolated lm_head + argmax over the tied [151936, 1024] table, two copies alternated
+    (622 MB > the 256 MB MALL); median time per call of --steps x 100 calls."""
+    import torch
+
+    import qwen_weights as qw
+    import qwen_megakernel_C as ext
+
+    hw = qw.host_weights(seed=0, std=0.02)
+    W = [torch.from_numpy(hw.embed).cuda(), torch.from_numpy(hw.embed).cuda()]
+    g = torch.Generator(device="cuda").manual_seed(1000)
+    H = torch.randn(64, 1024, device="cuda", generator=g).half()
+    ts = []
+    for rep in range(args.warmup + args.steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for k in range(100):
+            ext.lm_head_argmax(H[k % 64], W[k & 1])
+        e1.record()
+        torch.cuda.synchronize()
+        if rep >= args.warmup:
+            ts.append(e0.elapsed_time(e1) / 100)
+    assert ext.last_error() == 0
+    ms = _median(ts)
+    nbytes = 151936 * 1024 * 2 + 1024 * 2
+    return aux_line("isolated lm_head + argmax (C1): microseconds per call", round(ms * 1e3, 2), "us/call",
+                    False, "c1", {"rows": 151936, "hidden": 1024, "copies": 2}, "qwen_decode_kernel",
+                    nbytes, ms, args.steps, args.warmup)
+
+
+def run_mlp(args):
+    """C2: isolated MLP half-layer (RMSNorm, gate/up, SiLU*up, down, residual) rotating 16 weight
+    sets (302 MB > the 256 MB MALL); median time per call of --steps x 160 calls."""
+    import torch
+
+    import qwen_megakernel_C as ext
+
+    g = torch.Generator(device="cuda").manual_seed(7)
+    sets = []
+    for _ in range(16):
+        gate = (torch.randn(3072, 1024, device="cuda", generator=g) * 0.02).half()
+        up = (torch.randn(3072, 1024, device="cuda", generator=g) * 0.02).half()
+        down = (torch.randn(1024, 3072, device="cuda", generator=g) * 0.02).half()
+        sets.append((torch.ones(1024, device="cuda").half(), gate, up, down))
+    x = torch.randn(1024, device="cuda", generator=g).half()
+    ts = []
+    for rep in range(args.warmup + args.steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for k in range(160):
+            n, ga, u, d = sets[k % 16]
+            ext.mlp_block(x, n, ga, u, d)
+        e1.record()
+        torch.cuda.synchronize()
+        if rep >= args.warmup:
+            ts.append(e0.elapsed_time(e1) / 160)
+    assert ext.last_error() == 0
+    ms = _median(ts)
+    nbytes = 3 * 3072 * 1024 * 2 + 1024 * 2 + 2 * 1024 * 2
+    return aux_line("isolated MLP block (C2): microseconds per call", round(ms * 1e3, 2), "us/call", False, "c2",
+                    {"hidden": 1024, "inter": 3072, "weight_sets": 16}, "qwen_decode_kernel", nbytes, ms,
+                    args.steps, args.warmup)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,11 +218,20 @@ def main():
     ap.add_argument("--trace", default=None,
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
                          "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, events], 100 MHz ticks)")
+    ap.add_argument("--workload", choices=["c4", "c3", "c0", "c1", "c2"], default="c4",
+                    help="c4 (default): the headline decode at context 1921..2048; c3: 128-id prompt + "
+                         "generate_nosync 512; c0: 16 + 32; c1: isolated lm_head + argmax; c2: isolated MLP block")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine runs one sequence on one MI355X; --gpus {args.gpus} "
               "is not supported (independent sequences scale as one engine per GPU).", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "c4":
+        runs = {"c3": lambda: run_generate(args, 128, 512, "c3"), "c0": lambda: run_generate(args, 16, 32, "c0"),
+                "c1": lambda: run_lm_head(args), "c2": lambda: run_mlp(args)}
+        print(json.dumps(runs[args.workload]()), flush=True)
+        return
 
     import torch
 
