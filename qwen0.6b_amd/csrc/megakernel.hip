@@ -192,11 +192,6 @@ __device__ __forceinline__ float rows4_sum(float v) {
   return pack32(t, t);
 }
 __device__ __forceinline__ float rows4_max(float v) { return max32x(max16x(v)); }
-// value of lane ^ 16 (the partner row at the same position)
-__device__ __forceinline__ float xor16(float v) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return ((__lane_id() >> 4) & 1) ? __uint_as_float(r[0]) : __uint_as_float(r[1]);
-}
 // 4 row partials -> full sums: lanes 0-15 hold a, 16-31 c, 32-47 b, 48-63 d
 __device__ __forceinline__ float reduce4(float a, float b, float c, float d) {
   return row16_sum(pack16(pack32(a, b), pack32(c, d)));
@@ -434,7 +429,6 @@ __device__ __forceinline__ void trace_ev(const KParams& P, int token, int stage,
   }
 }
 
-__device__ __forceinline__ const v4u* ring_line(Shared* S, u32 n) { return S->ring[n % RING_LINES]; }
 // A stage's lines from its first global line n0: vb = this lane's byte offset of line n0
 // in the ring, and line n0 + k is at (vb + 1024 k) mod the ring size (the ring is the first
 // 128 KB of LDS), one add and one and per line
@@ -589,11 +583,6 @@ __device__ __forceinline__ void release_lines(CW& W, u32 end) {
 // per wave and gathered in LDS behind one four-wave barrier, which keeps each XCD's
 // polling traffic a quarter as large.
 
-// slots (2 s, 2 s + 1) of a b128 pair -> values 4 s .. 4 s + 3 of an H2 vector
-__device__ __forceinline__ void unpack8(v4u p, v4u q, float (&x)[8]) {
-  x[0] = lo_h(p.x); x[1] = hi_h(p.x); x[2] = lo_h(p.z); x[3] = hi_h(p.z);
-  x[4] = lo_h(q.x); x[5] = hi_h(q.x); x[6] = lo_h(q.z); x[7] = hi_h(q.z);
-}
 __device__ __forceinline__ float sumsq16(const float (&xa)[8], const float (&xb)[8]) {
   float s = 0.f;
 #pragma unroll
