@@ -38,7 +38,7 @@ int main() {
   CHECK(XCD_SLOTS % 2 == 0 && OFF_ARG % 2 == 0, "xcd / arg alignment");
   CHECK(xbuf(1, NXCD - 1, XCD_SLOTS) == OFF_ARG, "xcd buffers end at the ARG buffer");
   CHECK(OFF_ARG + 2L * ARG_SLOTS == TOTAL_SLOTS, "ARG end");
-  CHECK(TOTAL_SLOTS * 8 + 256 == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
+  CHECK(TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
   CHECK(BLOCK == 512 && NLOC == 32 && NXCD * NLOC == NWG, "grid constants");
   for (int w = 0; w < NWG; ++w) CHECK(8 * loc_of(w) + xcd_of(w) == w, "w = 8 i + x");
 
@@ -379,6 +379,21 @@ int main() {
           seen[r]++;
         }
     for (int r = 0; r < VOCAB; ++r) CHECK(seen[r] == 1, "lm row %d seen %d", r, seen[r]);
+    // with the pool: the workgroups' first LM_STATIC chunks and the pool's LM_POOL chunks
+    std::vector<int> seen2(LM_NCHUNK, 0);
+    for (int w = 0; w < NWG; ++w)
+      for (int ch = 0; ch < LM_STATIC; ++ch) {
+        CHECK(ch < lm_chunks(w), "static chunk is dealt");
+        seen2[w + NWG * ch]++;
+      }
+    CHECK(LM_GROUP * LM_NGRP == NWG && LM_NGRP <= WAVE, "pool groups");
+    for (int G = 0; G < LM_NGRP; ++G)
+      for (int k = 0; k < lm_group_chunks(G); ++k) {
+        const int g = LM_STATIC * NWG + LM_NGRP * k + G;
+        CHECK(g >= LM_STATIC * NWG && g < LM_NCHUNK, "pool chunk range");
+        seen2[g]++;
+      }
+    for (int g = 0; g < LM_NCHUNK; ++g) CHECK(seen2[g] == 1, "lm chunk %d seen %d", g, seen2[g]);
     // ARG: workgroup w stores slots 2w, 2w + 1; quarter c polls pairs 64 c + lane
     for (int c = 0; c < NCW; ++c)
       for (int lane = 0; lane < WAVE; ++lane) {

@@ -305,6 +305,7 @@ struct Shared {
   u32 xfin_cnt;                    // quarters of xfin stored (monotonic)
   u32 lm_cnt;                      // lm_head partials stored (monotonic)
   u32 lm_next[2];                  // next lm_head chunk of the workgroup (by phase parity)
+  u32 lm_pool_done[2];             // the pool ran out (by phase parity)
   u32 abort;
   // the layer pointer table, copied from global memory at start: reading it from
   // LDS keeps the loader waves' vmcnt free of anything but their own DMAs
@@ -438,20 +439,20 @@ __device__ __forceinline__ v4u ring_ld(const Shared* S, u32 vb, int k) {
 }
 
 // ------------------------------------------------------------------------------------
-// lm_head rows (every wave): the workgroup's 8-row chunks of the tied embedding, two
-// chunks in registers per wave, dotted with xfin (fp32)
+// lm_head rows (every wave): 8-row chunks of the tied embedding (the workgroup's own,
+// then claimed from the pool), two chunks in registers per wave, dotted with xfin (fp32)
 
-__device__ __forceinline__ void lm_issue(const KParams& P, int w, int ch, v4u (&buf)[16]) {
+__device__ __forceinline__ void lm_issue(const KParams& P, int g, v4u (&buf)[16]) {
   const int lane = __lane_id();
 #pragma unroll
   for (int j = 0; j < LM_CHUNK; ++j) {
-    const _Float16* base = P.lm_head + (long)lm_row(w, ch, j) * HIDDEN;
+    const _Float16* base = P.lm_head + (long)(LM_CHUNK * g + j) * HIDDEN;
     buf[2 * j] = ld_nt(base + 8 * lane);
     buf[2 * j + 1] = ld_nt(base + 512 + 8 * lane);
   }
 }
 
-__device__ __forceinline__ void lm_consume(const KParams& P, int w, int ch, int t, const v4u (&buf)[16],
+__device__ __forceinline__ void lm_consume(const KParams& P, int g, int t, const v4u (&buf)[16],
                                            const float (&a)[8], const float (&b)[8], float& best, int& bidx) {
   const int lane = __lane_id();
   float part[8];
@@ -459,17 +460,17 @@ __device__ __forceinline__ void lm_consume(const KParams& P, int w, int ch, int 
   for (int j = 0; j < LM_CHUNK; ++j) part[j] = dot8(buf[2 * j], a) + dot8(buf[2 * j + 1], b);
   float y0, y1;
   reduce8(part, y0, y1);
-  // lanes 0, 16, 32, 48 hold rows (0, 4), (2, 6), (1, 5), (3, 7): each lane's rows ascend
-  // over the token, so a strict > keeps the lowest index among equal logits
+  // lanes 0, 16, 32, 48 hold rows (0, 4), (2, 6), (1, 5), (3, 7); chunks arrive in no
+  // particular order, so equal logits keep the lower row explicitly
   if ((lane & 15) == 0) {
     const int jr = reduce8_row(lane);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int row = lm_row(w, ch, jr + 4 * h);
+      const int row = LM_CHUNK * g + jr + 4 * h;
       const float val = h == 0 ? y0 : y1;
       if (P.logits_out) P.logits_out[(long)t * VOCAB + row] = val;
       const float vv = __builtin_isnan(val) ? -INFINITY : val;
-      if (vv > best) {
+      if (vv > best || (vv == best && row < bidx)) {
         best = vv;
         bidx = row;
       }
@@ -484,16 +485,72 @@ __device__ __forceinline__ int lm_grab(Shared* S, u32 phase) {
   return (int)__builtin_amdgcn_readfirstlane(ch);
 }
 
-__device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, u32 phase) {
+// pool counter of group G for token epoch e: (epoch << 32) + chunks claimed so far.
+// Workgroup 0 sets the counters of epochs e + 2 and e + 3 during token e, when every claim
+// of tokens e - 2 and e - 1 (same counters) has returned; a counter whose epoch differs
+// is not in use.
+__device__ __forceinline__ u64* lm_pool_ctr(const KParams& P, u32 e, int G) {
+  return (u64*)((char*)P.status + 256 + ((e & 3) * LM_NGRP + G) * LM_CTR_STRIDE);
+}
+
+struct LmClaim {
+  int ch;     // the workgroup's chunk counter value
+  bool pool;  // a pool claim was sent
+  u64 r;      // its result (lane 0)
+};
+
+// claim the wave's next chunk: the workgroup's own chunks first, then the pool (the
+// device-scope add is sent now and read at lm_take, one chunk later)
+__device__ __forceinline__ LmClaim lm_claim(const KParams& P, Shared* S, u32 phase, u32 epoch) {
+  LmClaim c;
+  c.ch = lm_grab(S, phase);
+  c.pool = c.ch >= LM_STATIC && lds_ld(&S->lm_pool_done[phase & 1]) == 0u;
+  c.r = 0;
+  if (c.pool && __lane_id() == 0) {
+    // a per-lane address keeps the atomic optimizer from rewriting the add into a
+    // wave-wide one whose result is read (and waited for) right where it is sent
+    __attribute__((address_space(1))) u64* ctr =
+        (__attribute__((address_space(1))) u64*)lm_pool_ctr(P, epoch, blockIdx.x / LM_GROUP);
+    asm volatile("" : "+v"(ctr));
+    c.r = __hip_atomic_fetch_add(ctr, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return c;
+}
+
+// the claimed chunk id, or -1 when the wave is done
+__device__ __forceinline__ int lm_take(Shared* S, const LmClaim& c, int w, u32 phase, u32 epoch) {
+  if (c.ch < LM_STATIC) return w + NWG * c.ch;
+  if (!c.pool) return -1;  // the pool ran out
+  // read the claim here, not where it was sent: without the fence the compiler moves the
+  // lane-0 reads up to the add itself, which then waits for every load sent before it
+  u64 r = c.r;
+  asm volatile("" : "+v"(r));
+  const u32 lo = __builtin_amdgcn_readfirstlane((u32)r), hi = __builtin_amdgcn_readfirstlane((u32)(r >> 32));
+  if (hi == epoch) {
+    const int G = w / LM_GROUP;
+    if (lo < (u32)lm_group_chunks(G)) return LM_STATIC * NWG + LM_NGRP * (int)lo + G;
+    if (__lane_id() == 0) lds_st(&S->lm_pool_done[phase & 1], 1u);
+    return -1;
+  }
+  // the counter is not set up for this token: the workgroup's remaining dealt chunks
+  return c.ch < lm_chunks(w) ? w + NWG * c.ch : -1;
+}
+
+__device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, u32 phase, u32 epoch) {
   Shared* S = C.S;
   const int w = blockIdx.x, lane = __lane_id();
-  const int nch = lm_chunks(w);
-  // the next phase's counter is idle until every wave has passed this phase's xfin
-  // wait, and each wave reaches that wait only after its last grab of the previous phase
-  if (v == 0 && lane == 0) lds_st(&S->lm_next[(phase + 1) & 1], 0u);
+  // the next phase's counter and flag are idle until every wave has passed this phase's
+  // xfin wait, and each wave reaches that wait only after its last claim of the previous phase
+  if (v == 0 && lane == 0) {
+    lds_st(&S->lm_next[(phase + 1) & 1], 0u);
+    lds_st(&S->lm_pool_done[(phase + 1) & 1], 0u);
+  }
   v4u A[16], B[16];
-  int ca = lm_grab(S, phase);
-  if (ca < nch) lm_issue(P, w, ca, A);
+  // two chunks in flight (A, B); each buffer's next chunk is claimed right after its loads
+  // are sent, so a pool claim returns behind them and is read once they are consumed
+  int ga = lm_take(S, lm_claim(P, S, phase, epoch), w, phase, epoch);
+  if (ga >= 0) lm_issue(P, ga, A);
+  LmClaim na = lm_claim(P, S, phase, epoch);
   lds_wait_ge(C, &S->xfin_cnt, NCW * phase);
   float a[8], b[8];
   {
@@ -504,19 +561,27 @@ __device__ __forceinline__ void lm_rows(Ctl& C, const KParams& P, int v, int t, 
   }
   float best = -INFINITY;
   int bidx = 0x7fffffff;
-  // two chunks in flight (A, B); the older one is consumed first, and since grabs ascend,
-  // the first chunk id past the end means every later one is too
-  int cb = lm_grab(S, phase);
-  if (cb < nch) lm_issue(P, w, cb, B);
+  int gb = lm_take(S, lm_claim(P, S, phase, epoch), w, phase, epoch);
+  if (gb >= 0) lm_issue(P, gb, B);
+  LmClaim nb = lm_claim(P, S, phase, epoch);
   for (;;) {
-    if (ca >= nch) break;
-    lm_consume(P, w, ca, t, A, a, b, best, bidx);
-    ca = lm_grab(S, phase);
-    if (ca < nch) lm_issue(P, w, ca, A);
-    if (cb >= nch) break;
-    lm_consume(P, w, cb, t, B, a, b, best, bidx);
-    cb = lm_grab(S, phase);
-    if (cb < nch) lm_issue(P, w, cb, B);
+    if (ga >= 0) {
+      lm_consume(P, ga, t, A, a, b, best, bidx);
+      ga = lm_take(S, na, w, phase, epoch);
+      if (ga >= 0) {
+        lm_issue(P, ga, A);
+        na = lm_claim(P, S, phase, epoch);
+      }
+    }
+    if (gb >= 0) {
+      lm_consume(P, gb, t, B, a, b, best, bidx);
+      gb = lm_take(S, nb, w, phase, epoch);
+      if (gb >= 0) {
+        lm_issue(P, gb, B);
+        nb = lm_claim(P, S, phase, epoch);
+      }
+    }
+    if (ga < 0 && gb < 0) break;
   }
   wave_argmax(best, bidx);
   if (lane == 0) {
@@ -1183,7 +1248,7 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
     }
     st_lm_input(W, P, t, epoch);
     ++phase;
-    lm_rows(W.C, P, c, t, phase);
+    lm_rows(W.C, P, c, t, phase, epoch);
     trace_ev(P, t, NSTAGE * L, TR_SYNC);
     // workgroup partial -> ARG slots; every workgroup then reduces all 256
     if (c == 0) {
@@ -1192,6 +1257,12 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
       int bidx = 0x7fffffff;
 #pragma unroll
       for (int v = 0; v < NCW + NLW; ++v) better(best, bidx, S->lmv[v], S->lmi[v]);
+      if (W.w == 0 && W.lane < LM_NGRP) {  // set up the pool counters of tokens epoch + 2, epoch + 3
+#pragma unroll
+        for (u32 d = 2; d < 4; ++d)
+          __hip_atomic_store(lm_pool_ctr(P, epoch + d, W.lane), (u64)(epoch + d) << 32, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
       if (W.lane == 0) {
         const u32 tg = tag_arg(epoch);
         ll_store(P.ws, slot_arg(t & 1, 2 * W.w), __float_as_uint(best), tg);
@@ -1349,7 +1420,7 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
     }
     if (P.mode == MODE_MLP) break;
     ++phase;
-    lm_rows(C, P, NCW + q, t, phase);
+    lm_rows(C, P, NCW + q, t, phase, P.epoch0 + (u32)t);
     if (q == 0) trace_ev(P, t, NSTAGE * L, TR_MERGE);
   }
   if (!C.ok) lds_st(&S->abort, 1u);
@@ -1366,6 +1437,8 @@ __global__ void __launch_bounds__(BLOCK, 1) qwen_decode_kernel(KParams P) {
     S.lm_cnt = 0;
     S.lm_next[0] = 0;
     S.lm_next[1] = 0;
+    S.lm_pool_done[0] = 0;
+    S.lm_pool_done[1] = 0;
     S.abort = 0;
   }
   if (threadIdx.x < NLW) S.done_upto[threadIdx.x] = threadIdx.x;

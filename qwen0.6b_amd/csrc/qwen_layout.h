@@ -198,10 +198,25 @@ static_assert(VOCAB % LM_CHUNK == 0, "whole chunks");
 constexpr int LM_NCHUNK = VOCAB / LM_CHUNK;  // 18992
 // The vocabulary's 8-row chunks are dealt to the workgroups in turn (chunk g to workgroup
 // g mod NWG), so every workgroup streams rows from the whole table; a workgroup's 8 waves
-// take its chunks 0, 1, 2, .. in turn from a shared counter, so each wave's rows ascend.
+// take its chunks 0, 1, 2, .. in turn from a shared counter. Only its first LM_STATIC
+// chunks are its own. The chunks from LM_STATIC * NWG on form a pool, split over groups
+// of 8 consecutive workgroups (one per XCD): the waves of a group claim its share from a
+// device-scope counter once their own chunks are taken, so the group's workgroups on
+// faster XCDs take more of it. (When the counters are not set up for a token, each
+// workgroup takes all of its dealt chunks instead.)
 QL_HD int lm_chunks(int w) { return (LM_NCHUNK - w + NWG - 1) / NWG; }
 // lm_head row of workgroup w's chunk ch, slot j
 QL_HD int lm_row(int w, int ch, int j) { return LM_CHUNK * (w + NWG * ch) + j; }
+constexpr int LM_STATIC = 60;
+static_assert(LM_STATIC * NWG <= LM_NCHUNK, "every workgroup has LM_STATIC chunks");
+constexpr int LM_POOL = LM_NCHUNK - LM_STATIC * NWG;  // 3632
+constexpr int LM_GROUP = NXCD;                        // workgroups per pool group
+constexpr int LM_NGRP = NWG / LM_GROUP;               // 32
+// claim k of group G is pool chunk LM_STATIC * NWG + LM_NGRP * k + G
+QL_HD int lm_group_chunks(int G) { return (LM_POOL - G + LM_NGRP - 1) / LM_NGRP; }
+// pool counters: one 128-byte line per (token epoch mod 4, group), after the status line
+constexpr long LM_CTR_STRIDE = 128;
+constexpr long LM_CTR_BYTES = 4L * LM_NGRP * LM_CTR_STRIDE;
 
 // ---- exchange ("LL") buffers ---------------------------------------------------------
 // A slot is 8 bytes: 32 bits of payload + a 32-bit tag, written with one 8-byte
@@ -232,8 +247,8 @@ constexpr long B_DP = B_INT + INT_SLOTS;
 constexpr long XCD_SLOTS = B_DP + DP_SLOTS;   // 12032 per XCD per parity
 constexpr long OFF_ARG = 2L * NXCD * XCD_SLOTS;
 constexpr long TOTAL_SLOTS = OFF_ARG + 2L * ARG_SLOTS;
-// after the slots: one 256-byte line of status words
-constexpr long WORKSPACE_BYTES = TOTAL_SLOTS * 8 + 256;
+// after the slots: one 256-byte line of status words, then the lm_head pool counters
+constexpr long WORKSPACE_BYTES = TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES;
 
 // first slot of buffer `b` (one of B_*) of XCD x, parity par
 QL_HD long xbuf(int par, int x, long b) { return ((long)par * NXCD + x) * XCD_SLOTS + b; }

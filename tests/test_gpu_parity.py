@@ -268,6 +268,29 @@ def test_lm_head_argmax_1000_trials(ext, full):
         assert err < 1e-3, err
 
 
+def test_lm_head_exact_ties_lowest_index(ext, full):
+    """Exact ties resolve to the lowest row, whichever workgroup or claim order takes
+    the rows: pairs of identical rows (same row mod 8, so the same reduction path and
+    bit-identical logits) in the dealt part, across it and the claimed pool, and inside
+    the pool; h is the tied rows' own vector, so they beat every other row by far.
+    (The engine's first two tokens after its state is zeroed take all chunks as dealt
+    instead of claiming the pool; the earlier tests of this module cover those.)"""
+    hw, w, _ = full
+    W = w["embed_weight"].clone()
+    cases = [(15, 23), (7, 150007), (130007, 140007)]
+    for lo_row, hi_row in cases:
+        W[lo_row] = W[hi_row]
+    Wc = W.float().cpu()
+    for lo_row, hi_row in cases:
+        h = W[hi_row].clone()
+        ref = int(torch.argmax(Wc @ h.float().cpu()))
+        assert ref == lo_row  # torch: first of equal maxima
+        for _ in range(3):
+            got = int(ext.lm_head_argmax(h, W).cpu()[0])
+            assert got == lo_row, (lo_row, hi_row, got)
+    assert ext.last_error() == 0
+
+
 def test_mlp_block(ext, full):
     """Isolated MLP half-layer (RMSNorm, gate/up [6144,1024], SiLU*up, down, residual)."""
     hw, w, _ = full
