@@ -119,6 +119,20 @@ int qwen_generate_ex(
     float* hidden_steps, int num_layers, int start_position, int max_seq_len,
     float attn_scale, hipStream_t stream);
 
+/* generate_nosync that ends after the first step whose argmax is eos_token_id
+ * (no counterpart in the reference, which truncates on the host after all
+ * num_steps: Model/Qwen06B_architecture.py:379-381). output_log[0 .. n) receives
+ * the generated ids, the last one eos_token_id when it was reached, where
+ * n = *out_count (device int32) <= num_steps; later entries are not written. The
+ * K/V cache holds positions start_position .. start_position + n - 1. */
+int qwen_generate_until(
+    int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_normalized,
+    int* output_log, int* out_count, int num_layers, int start_position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */

@@ -45,7 +45,7 @@ VOCAB_SIZE = 151936
 ROPE_THETA = 1_000_000.0  # Qwen3-0.6B config.json "rope_theta"
 DEVICE = "cuda"  # where Decoder allocates its state; the engine itself needs the GPU
 
-_OPS = ("decode", "generate_nosync")
+_OPS = ("decode", "generate_nosync", "generate_until")
 
 
 def _require_megakernel_op(op_name: str):
@@ -322,13 +322,32 @@ class Decoder:
         _check_device_errors()
         return last
 
-    def generate_ids(self, ids, max_tokens: int = 100) -> list:
+    def generate_until(self, first_token_id: int, max_tokens: int, eos_token_id: int) -> list:
+        """Up to ``max_tokens`` greedy steps in one launch that end on the device after the
+        first ``eos_token_id`` (included in the result); advances the position by the
+        number of steps run."""
+        if self._position + max_tokens > MAX_SEQ_LEN:
+            raise RuntimeError(f"positions {self._position}..{self._position + max_tokens} exceed {MAX_SEQ_LEN}")
+        gen = _require_megakernel_op("generate_until")
+        out, count = gen(int(first_token_id), int(max_tokens), int(eos_token_id), self._embed_weight,
+                         self._layer_weights_packed, self._final_norm_weight, self._lm_head_weight, self._cos_table,
+                         self._sin_table, self._k_cache, self._v_cache, self._hidden, self._norm_out,
+                         self._num_layers, self._position, MAX_SEQ_LEN, self._attn_scale)
+        n = int(count.item())
+        _check_device_errors()
+        self._position += n
+        return out[:n].cpu().tolist()
+
+    def generate_ids(self, ids, max_tokens: int = 100, eos_token_id=None) -> list:
         """Greedy generation on token ids (reference ``generate`` without the tokenizer):
-        prefill ids[:-1], then ``max_tokens`` on-device steps from ids[-1]."""
+        prefill ids[:-1], then ``max_tokens`` on-device steps from ids[-1]; with
+        ``eos_token_id`` the device stops after that id (which ends the list)."""
         self.reset()
         ids = [int(t) for t in ids]
         if len(ids) > 1:
             self.prefill(ids[:-1])
+        if eos_token_id is not None:
+            return self.generate_until(ids[-1], max_tokens, eos_token_id)
         out = self.generate_nosync(ids[-1], max_tokens).cpu().tolist()
         _check_device_errors()
         return out
@@ -337,8 +356,8 @@ class Decoder:
         if self.tokenizer is None:
             raise RuntimeError("generate(prompt) needs a tokenizer; use generate_ids() for token ids")
         ids = self.tokenizer.encode(prompt, add_special_tokens=True)
-        out = self.generate_ids(ids, max_tokens)
         eos = self.tokenizer.eos_token_id
+        out = self.generate_ids(ids, max_tokens, eos_token_id=eos)
         if eos in out:
             out = out[: out.index(eos)]
         return self.tokenizer.decode(out, skip_special_tokens=True)

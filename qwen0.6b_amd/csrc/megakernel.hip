@@ -92,6 +92,8 @@ struct KParams {
   u64 deadline;            // wall-clock ticks a single wait may take
   u64* trace;              // nullable [NWG][trace_stages(L)][TRACE_EVENTS]
   int trace_token;         // token index whose stages are traced
+  int* out_count;          // nullable: steps run (the generation stops after eos)
+  int eos;                 // stop after the first step whose argmax is this id (-1: never)
   int mode, num_layers, first_token, start_pos, num_steps, max_seq;
   float attn_scale;
   u32 epoch0;
@@ -1289,7 +1291,13 @@ __device__ __forceinline__ void compute_wave(const KParams& P, Shared* S, int c)
       if (bidx < 0 || bidx >= VOCAB) bidx = 0;  // every logit NaN
       if (W.w == 0 && c == 0 && W.lane == 0) P.out_tokens[t] = bidx;
       trace_ev(P, t, NSTAGE * L, TR_STORE);
+      // every workgroup reduced the same 256 partials, so all of them stop at the same step
+      const bool stop = bidx == P.eos;
+      if (P.out_count && W.w == 0 && c == 0 && W.lane == 0 && (stop || t + 1 == P.num_steps)) *P.out_count = t + 1;
       token = (P.forced && t + 1 < P.num_steps) ? P.forced[t + 1] : bidx;
+      // the loader waves wait for ring space in the next step: the workgroup's abort flag
+      // (set below) ends that wait, and they leave without a device-side error
+      if (stop) W.C.ok = false;
       if (token < 0 || token >= VOCAB) {  // a forced id out of range: report and stop
         __hip_atomic_fetch_or(P.status, ST_BAD_TOKEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         W.C.ok = false;
@@ -1418,7 +1426,7 @@ __device__ __forceinline__ void loader_wave(const KParams& P, Shared* S, int q) 
       wait_vmcnt<0>();
       if (pending > 0) lds_st(&S->done_upto[q], last + 4);
     }
-    if (P.mode == MODE_MLP) break;
+    if (P.mode == MODE_MLP || !C.ok) break;
     ++phase;
     lm_rows(C, P, NCW + q, t, phase, P.epoch0 + (u32)t);
     if (q == 0) trace_ev(P, t, NSTAGE * L, TR_MERGE);
@@ -1552,6 +1560,7 @@ int fill_decode(KParams& P, const void* embed, const LDGLayerWeight* lw, const v
       (long)start + steps > (long)max_seq || max_seq > MAX_SEQ_LIMIT)
     return QWEN_ERR_ARG;
   memset(&P, 0, sizeof(P));
+  P.eos = -1;
   P.embed = (const _Float16*)embed;
   P.layers = lw;
   P.final_norm = (const _Float16*)fnorm;
@@ -1625,6 +1634,27 @@ extern "C" int qwen_generate_ex(int first_token_id, int num_steps, const int* fo
   return launch(P, stream);
 }
 
+extern "C" int qwen_generate_until(int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
+                                   const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+                                   const void* lm_head_weight, const void* cos_table, const void* sin_table,
+                                   void* k_cache, void* v_cache, void* hidden_buffer, void* g_normalized,
+                                   int* output_log, int* out_count, int num_layers, int start_position,
+                                   int max_seq_len, float attn_scale, hipStream_t stream) {
+  KParams P;
+  int rc = fill_decode(P, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                       k_cache, v_cache, hidden_buffer, g_normalized, num_layers, start_position, num_steps,
+                       max_seq_len, attn_scale);
+  if (rc != QWEN_OK) return rc;
+  if (!output_log || !out_count || first_token_id < 0 || first_token_id >= VOCAB || eos_token_id < 0 ||
+      eos_token_id >= VOCAB)
+    return QWEN_ERR_ARG;
+  P.first_token = first_token_id;
+  P.out_tokens = output_log;
+  P.out_count = out_count;
+  P.eos = eos_token_id;
+  return launch(P, stream);
+}
+
 extern "C" int launch_ldg_generate_nosync(int first_token_id, int num_steps, const void* embed_weight,
                                           const LDGLayerWeight* layer_weights, const void* final_norm_weight,
                                           const void* lm_head_weight, const void* cos_table, const void* sin_table,
@@ -1643,6 +1673,7 @@ extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, i
   if (logits_out && !aligned16(logits_out)) return QWEN_ERR_ARG;
   KParams P;
   memset(&P, 0, sizeof(P));
+  P.eos = -1;
   P.lm_head = (const _Float16*)weight;
   P.in_vec = (const _Float16*)hidden_f16;
   P.out_tokens = out_token;
@@ -1678,6 +1709,7 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
   if (hipStreamSynchronize(stream) != hipSuccess) return QWEN_ERR_LAUNCH;
   KParams P;
   memset(&P, 0, sizeof(P));
+  P.eos = -1;
   P.layers = d_tab[dev];
   P.in_vec = (const _Float16*)x_f16;
   P.out_vec = y_out;

@@ -13,6 +13,7 @@
 
 #include <cstdint>
 #include <string>
+#include <tuple>
 
 #include "qwen_megakernel.h"
 
@@ -158,6 +159,33 @@ torch::Tensor generate_ex(int first_token_id, int num_steps, c10::optional<torch
   return out;
 }
 
+// generate_nosync that ends at eos_token_id; returns (ids int32[num_steps], count int32[1]),
+// both on the device: ids[0 .. count) were generated, the rest are -1
+std::tuple<torch::Tensor, torch::Tensor> generate_until(int first_token_id, int num_steps, int eos_token_id,
+                                                        torch::Tensor embed_weight, torch::Tensor layer_weights_packed,
+                                                        torch::Tensor final_norm_weight, torch::Tensor lm_head_weight,
+                                                        torch::Tensor cos_table, torch::Tensor sin_table,
+                                                        torch::Tensor k_cache, torch::Tensor v_cache,
+                                                        torch::Tensor hidden, torch::Tensor norm_out, int num_layers,
+                                                        int start_position, int max_seq_len, float attn_scale) {
+  const LDGLayerWeight* tab = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight,
+                                           cos_table, sin_table, k_cache, v_cache, hidden, norm_out, num_layers,
+                                           max_seq_len);
+  TORCH_CHECK(first_token_id >= 0 && first_token_id < V, "first_token_id ", first_token_id, " out of range");
+  TORCH_CHECK(eos_token_id >= 0 && eos_token_id < V, "eos_token_id ", eos_token_id, " out of range");
+  TORCH_CHECK(num_steps >= 1, "num_steps must be >= 1");
+  TORCH_CHECK(start_position >= 0 && (int64_t)start_position + num_steps <= max_seq_len, "positions exceed max_seq_len");
+  auto out = torch::full({num_steps}, -1, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  auto count = torch::zeros({1}, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  const int rc = qwen_generate_until(first_token_id, num_steps, eos_token_id, embed_weight.data_ptr(), tab,
+                                     final_norm_weight.data_ptr(), lm_head_weight.data_ptr(), cos_table.data_ptr(),
+                                     sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), hidden.data_ptr(),
+                                     norm_out.data_ptr(), out.data_ptr<int>(), count.data_ptr<int>(), num_layers,
+                                     start_position, max_seq_len, attn_scale, stream_of(embed_weight));
+  check_rc(rc, "generate_until");
+  return {out, count};
+}
+
 torch::Tensor lm_head_argmax(torch::Tensor hidden, torch::Tensor weight, c10::optional<torch::Tensor> logits_out) {
   check_dev(hidden, "hidden", torch::kHalf, H);
   check_dev(weight, "weight", torch::kHalf, V * H);
@@ -212,6 +240,13 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
         pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("hidden"), pybind11::arg("norm_out"),
         pybind11::arg("logits_out"), pybind11::arg("hidden_steps"), pybind11::arg("num_layers"),
         pybind11::arg("start_position"), pybind11::arg("max_seq_len"), pybind11::arg("attn_scale"));
+  m.def("generate_until", &generate_until, "on-device greedy generation that ends at eos_token_id",
+        pybind11::arg("first_token_id"), pybind11::arg("num_steps"), pybind11::arg("eos_token_id"),
+        pybind11::arg("embed_weight"), pybind11::arg("layer_weights_packed"), pybind11::arg("final_norm_weight"),
+        pybind11::arg("lm_head_weight"), pybind11::arg("cos_table"), pybind11::arg("sin_table"),
+        pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("hidden"), pybind11::arg("norm_out"),
+        pybind11::arg("num_layers"), pybind11::arg("start_position"), pybind11::arg("max_seq_len"),
+        pybind11::arg("attn_scale"));
   m.def("lm_head_argmax", &lm_head_argmax, "isolated lm_head GEMV + argmax", pybind11::arg("hidden"),
         pybind11::arg("weight"), pybind11::arg("logits_out") = pybind11::none());
   m.def("mlp_block", &mlp_block, "isolated RMSNorm + SwiGLU MLP + residual");

@@ -237,6 +237,27 @@ def test_decode_is_deterministic_and_matches_generate(ext, full, qa):
     assert stepped == a[0]
 
 
+def test_generate_until_stops_at_eos(ext, full, qa):
+    """On-device end of generation: with eos = the id the free-running greedy sequence
+    first produces at step k, generate_until returns exactly the first k + 1 ids, advances
+    the position by k + 1, and leaves the K/V cache so that the next step continues the
+    sequence; with an eos that never comes it runs every step."""
+    hw, w, packed = full
+    dec = qa.Decoder(weights=w, verbose=False)
+    prompt = [int(t) for t in np.random.Generator(np.random.PCG64(7)).integers(0, V, 12)]
+    n = 24
+    ref = dec.generate_ids(prompt, n)
+    k = next(i for i in range(3, n - 1) if ref[i] not in ref[:i])
+    got = dec.generate_ids(prompt, n, eos_token_id=ref[k])
+    assert got == ref[:k + 1]
+    assert dec.position == len(prompt) - 1 + k + 1
+    assert dec.step(ref[k]) == ref[k + 1]
+    absent = next(t for t in range(V) if t not in ref)
+    assert dec.generate_ids(prompt, n, eos_token_id=absent) == ref
+    assert dec.position == len(prompt) - 1 + n
+    assert ext.last_error() == 0
+
+
 def test_lm_head_argmax_1000_trials(ext, full):
     """Isolated lm_head + argmax: W = the seed-0 embedding [151936, 1024],
     h_t ~ N(0, 1) fp16 (PCG64 seed 1000 + t), 1000 trials."""

@@ -66,6 +66,18 @@ class OracleStub(types.ModuleType):
             out.append(tok)
         return torch.tensor(out, dtype=torch.int32)
 
+    def generate_until(self, first, n, eos, *args):
+        num_layers, start, max_seq, scale = args[-4:]
+        self.calls.append(("generate_until", first, start, n, eos))
+        out, tok = [], first
+        for s in range(n):
+            tok = self.oracle.step(tok, start + s)["token"]
+            out.append(tok)
+            if tok == eos:
+                break
+        count = len(out)
+        return torch.tensor(out + [-1] * (n - count), dtype=torch.int32), torch.tensor([count], dtype=torch.int32)
+
     def generate_ex(self, first, n, forced, *args):
         num_layers, start, max_seq, scale = args[-4:]
         self.calls.append(("generate_ex", first, start, n))
@@ -171,6 +183,18 @@ def test_generate_text_truncates_at_eos(qa_cpu, small_hw):
     dec = mod.Decoder(weights=_weights(mod), tokenizer=Tok(), verbose=False)
     first = ref.index(ref[2])
     assert dec.generate("hi", 5) == ",".join(map(str, ref[:first]))
+
+
+def test_generate_ids_stops_at_eos(qa_cpu, small_hw):
+    mod, stub = qa_cpu
+    prompt = [3, 1, 4, 1, 5]
+    ref = orc.Oracle(small_hw).greedy(prompt, 8)["tokens"]
+    k = next(i for i in range(2, 8) if ref[i] not in ref[:i])
+    dec = mod.Decoder(weights=_weights(mod), verbose=False)
+    out = dec.generate_ids(prompt, 8, eos_token_id=ref[k])
+    assert out == ref[:k + 1]
+    assert stub.calls[-1] == ("generate_until", 5, 4, 8, ref[k])
+    assert dec.position == len(prompt) - 1 + k + 1
 
 
 def test_positions_past_the_cache_raise(qa_cpu):
