@@ -723,6 +723,10 @@ __device__ __forceinline__ void gain_act(const float (&xa)[8], const float (&xb)
 __device__ __forceinline__ float row2k(const Shared* S, u32 vb, int k, const float (&a)[8], const float (&b)[8]) {
   return dot8(ring_ld(S, vb, k), a) + dot8(ring_ld(S, vb, k + 1), b);
 }
+// the same for a row already read from the ring into registers
+__device__ __forceinline__ float row2k_r(const v4u& w0, const v4u& w1, const float (&a)[8], const float (&b)[8]) {
+  return dot8(w0, a) + dot8(w1, b);
+}
 
 // ---- stages ----------------------------------------------------------------------------
 
@@ -734,24 +738,35 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   const u32 n0 = W.gl;  // lines n0, n0 + 1: input norm weights; then the rows
   W.gl += LINES_QKV;
   float xa[8], xb[8], ss;
+  const u32 vb = ring_vbase(n0, lane);
+  // the wave's ring lines (norm weights, 4 rows) are read into registers while it waits for
+  // its input, so no LDS latency follows the input's arrival
+  v4u wl[LINES_NORM + 8];
+  auto lines = [&] {
+    wait_lines(W, W.gl);
+    trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
+    wl[0] = ring_ld(S, vb, 0);
+    wl[1] = ring_ld(S, vb, 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wl[LINES_NORM + 2 * r] = ring_ld(S, vb, LINES_NORM + 2 * (4 * W.c + r));
+      wl[LINES_NORM + 2 * r + 1] = ring_ld(S, vb, LINES_NORM + 2 * (4 * W.c + r) + 1);
+    }
+  };
   if (l == 0) {
     const _Float16* row = P.embed + (long)token * HIDDEN;
     ss = load_x1024(row, lane, xa, xb);
     if (lane < 8) S->resid[8 * W.c + lane] = (float)row[HROWS * W.i + 8 * W.c + lane];
-    wait_lines(W, W.gl);
+    lines();
   } else {
-    ss = poll_x1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), xa, xb, [&] {
-      wait_lines(W, W.gl);
-      trace_ev(P, t, NSTAGE * l + S_QKV, TR_LINES);
-    });
+    ss = poll_x1024(W, tag_of(epoch, l - 1, S_DSUM), xbuf(par ^ 1, W.x, B_X), xa, xb, lines);
   }
   trace_ev(P, t, NSTAGE * l + S_QKV, TR_INPUT);
   float a[8], b[8];
-  const u32 vb = ring_vbase(n0, lane);
-  gain_act(xa, xb, __builtin_bit_cast(h8, ring_ld(S, vb, 0)), __builtin_bit_cast(h8, ring_ld(S, vb, 1)), a, b);
+  gain_act(xa, xb, __builtin_bit_cast(h8, wl[0]), __builtin_bit_cast(h8, wl[1]), a, b);
   float part[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) part[r] = row2k(S, vb, LINES_NORM + 2 * (4 * W.c + r), a, b);
+  for (int r = 0; r < 4; ++r) part[r] = row2k_r(wl[LINES_NORM + 2 * r], wl[LINES_NORM + 2 * r + 1], a, b);
   release_lines(W, W.gl);
   // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
   const float rs = reduce4(part[0], part[1], part[2], part[3]) * rstd_of(ss);
@@ -1001,6 +1016,10 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   const u32 n0 = W.gl;
   W.gl += LINES_O;
   v4u a;  // attention output values [8 (lane % 32), +8), fp16 as exchanged
+  // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63); read into
+  // registers while the wave waits for its input
+  const u32 vb = ring_vbase(n0, lane);
+  v4u wl[4];
   {
     const int voff[2] = {32 * (lane & 31), 32 * (lane & 31) + 16};
     v4u v[2];
@@ -1008,15 +1027,15 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) wl[m] = ring_ld(S, vb, 4 * W.c + m);
     });
     a = v4u{v[0].x, v[0].z, v[1].x, v[1].z};
   }
   trace_ev(P, t, NSTAGE * l + S_O, TR_INPUT);
-  // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63)
   float part[4];
-  const u32 vb = ring_vbase(n0, lane);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) part[m] = dot8h(ring_ld(S, vb, 4 * W.c + m), a);
+  for (int m = 0; m < 4; ++m) part[m] = dot8h(wl[m], a);
   release_lines(W, W.gl);
   // y0 rows: (line 0 lo, line 1 lo, line 0 hi, line 1 hi) = rows 8c + (0, 2, 1, 3); y1 = +4
   const float y0 = row16_sum(pack16(part[0], part[1])), y1 = row16_sum(pack16(part[2], part[3]));
@@ -1087,26 +1106,39 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   const u32 n0 = W.gl;  // lines n0, n0 + 1: post-attention norm weights; then gate rows, up rows
   W.gl += LINES_GU;
   float xa[8], xb[8], ss;
+  const u32 vb = ring_vbase(n0, lane);
+  constexpr int ng = LINES_NORM;
+  // norm weights, then gate rows (wl[ng + 2 jj ..]) and up rows (wl[ng + 6 + 2 jj ..]),
+  // read into registers while the wave waits for its input
+  v4u wl[ng + 12];
+  auto lines = [&] {
+    wait_lines(W, W.gl);
+    trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
+    wl[0] = ring_ld(S, vb, 0);
+    wl[1] = ring_ld(S, vb, 1);
+#pragma unroll
+    for (int jj = 0; jj < 3; ++jj) {
+      wl[ng + 2 * jj] = ring_ld(S, vb, ng + 2 * (3 * W.c + jj));
+      wl[ng + 2 * jj + 1] = ring_ld(S, vb, ng + 2 * (3 * W.c + jj) + 1);
+      wl[ng + 6 + 2 * jj] = ring_ld(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj));
+      wl[ng + 6 + 2 * jj + 1] = ring_ld(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj) + 1);
+    }
+  };
   if (P.mode == MODE_MLP) {
     ss = load_x1024(P.in_vec, lane, xa, xb);
     if (lane < 8) S->actres[8 * W.c + lane] = (float)P.in_vec[HROWS * W.i + 8 * W.c + lane];
-    wait_lines(W, W.gl);
+    lines();
   } else {
-    ss = poll_x1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), xa, xb, [&] {
-      wait_lines(W, W.gl);
-      trace_ev(P, t, NSTAGE * l + S_GU, TR_LINES);
-    });
+    ss = poll_x1024(W, tag_of(epoch, l, S_OSUM), xbuf(par, W.x, B_ACT), xa, xb, lines);
   }
   trace_ev(P, t, NSTAGE * l + S_GU, TR_INPUT);
   float a[8], b[8];
-  const u32 vb = ring_vbase(n0, lane);
-  gain_act(xa, xb, __builtin_bit_cast(h8, ring_ld(S, vb, 0)), __builtin_bit_cast(h8, ring_ld(S, vb, 1)), a, b);
-  constexpr int ng = LINES_NORM;
+  gain_act(xa, xb, __builtin_bit_cast(h8, wl[0]), __builtin_bit_cast(h8, wl[1]), a, b);
   float part[6];
 #pragma unroll
   for (int jj = 0; jj < 3; ++jj) {
-    part[jj] = row2k(S, vb, ng + 2 * (3 * W.c + jj), a, b);                          // gate
-    part[3 + jj] = row2k(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj), a, b);      // up
+    part[jj] = row2k_r(wl[ng + 2 * jj], wl[ng + 2 * jj + 1], a, b);              // gate
+    part[3 + jj] = row2k_r(wl[ng + 6 + 2 * jj], wl[ng + 6 + 2 * jj + 1], a, b);  // up
   }
   release_lines(W, W.gl);
   float pq, qq;
@@ -1135,6 +1167,8 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   const u32 n0 = W.gl;
   W.gl += LINES_DOWN;
   v4u a;
+  const u32 vb = ring_vbase(n0, lane);
+  v4u wl[8];  // the wave's 8 lines, read into registers while it waits for its input
   {
     // wave c polls slot pairs k = 32 c + lane (lanes < 32): workgroup k / 4, wave k % 4 ->
     // inter values 12 (k / 4) + 3 (k % 4) + {0, 1, 2} (the pair's last half is padding),
@@ -1145,6 +1179,8 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) wl[r] = ring_ld(S, vb, 8 * W.c + r);
     });
     if (lane < 32) {
       const int k = 32 * W.c + lane;
@@ -1163,9 +1199,8 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   }
   trace_ev(P, t, NSTAGE * l + S_DOWN, TR_INPUT);
   float part[8];
-  const u32 vb = ring_vbase(n0, lane);
 #pragma unroll
-  for (int r = 0; r < 8; ++r) part[r] = dot8h(ring_ld(S, vb, 8 * W.c + r), a);
+  for (int r = 0; r < 8; ++r) part[r] = dot8h(wl[r], a);
   release_lines(W, W.gl);
   float y0, y1;
   reduce8(part, y0, y1);
