@@ -793,6 +793,16 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   // dm, dm + 1 and their rotate-half partners 64 + dm, 65 + dm of q head h, and of k (h = 0)
   // or v (h = 1), so RoPE needs no other lane
   const int dm = 2 * (lane & 31), hb = 128 * (lane >> 5) + dm;
+  const u32 nkl = n0 + LINES_ATTMISC;  // first K line
+  const u32 vbk = ring_vbase(nkl, lane);
+  // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..; a wave whose lines run
+  // past the split's last (m >= nk) reads that last line again (or, for an empty split, the
+  // misc line), which holds finite values; those positions are masked out of the softmax
+  const int j = lane >> 4, q16 = lane & 15;
+  // the norm / cos / sin values and the wave's K and V lines are read into registers while
+  // the wave waits for its input
+  h2 qn0, qn1, kn0, kn1, cv0, cv1, sv0, sv1;
+  v4u kw[4], vw[4];
   float2 qlo, qhi, klo, khi;
   {  // wave c polls slots [64 c, +64) (lane % 32: values 128 c + 4 (lane % 32) .. +4) into S->xs;
      // lanes 32-63 repeat lanes 0-31 (same lines, same values), which keeps the wave unbranched
@@ -802,6 +812,21 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
             [&] {
       wait_lines(W, W.gl);
       trace_ev(P, t, NSTAGE * l + S_ATT, TR_LINES);
+      const char* misc = (const char*)S->ring[n0 % RING_LINES];
+      qn0 = *(const h2*)(misc + 2 * dm);
+      qn1 = *(const h2*)(misc + 2 * (64 + dm));
+      kn0 = *(const h2*)(misc + 256 + 2 * dm);
+      kn1 = *(const h2*)(misc + 256 + 2 * (64 + dm));
+      cv0 = *(const h2*)(misc + 512 + 2 * dm);
+      cv1 = *(const h2*)(misc + 512 + 2 * (64 + dm));
+      sv0 = *(const h2*)(misc + 768 + 2 * dm);
+      sv1 = *(const h2*)(misc + 768 + 2 * (64 + dm));
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) {
+        const int mm = nk > 0 ? min(4 * W.c + bb, nk - 1) : -LINES_ATTMISC;
+        kw[bb] = ring_ld(S, vbk, mm);
+        vw[bb] = ring_ld(S, vbk, (nk > 0 ? nk : 0) + mm);
+      }
     });
     *(float4*)(S->xs + 128 * W.c + 4 * (lane & 31)) =
         make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
@@ -812,15 +837,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     khi = *(const float2*)(S->xs + 256 + hb + 64);
   }
   trace_ev(P, t, NSTAGE * l + S_ATT, TR_INPUT);
-  const u32 nkl = n0 + LINES_ATTMISC;  // first K line
-  const u32 vbk = ring_vbase(nkl, lane);
   // every wave computes the normed, roped q0 | q1 | k and v into its own scratch
   {
-    const char* misc = (const char*)S->ring[n0 % RING_LINES];
-    const h2 qn0 = *(const h2*)(misc + 2 * dm), qn1 = *(const h2*)(misc + 2 * (64 + dm));
-    const h2 kn0 = *(const h2*)(misc + 256 + 2 * dm), kn1 = *(const h2*)(misc + 256 + 2 * (64 + dm));
-    const h2 cv0 = *(const h2*)(misc + 512 + 2 * dm), cv1 = *(const h2*)(misc + 512 + 2 * (64 + dm));
-    const h2 sv0 = *(const h2*)(misc + 768 + 2 * dm), sv1 = *(const h2*)(misc + 768 + 2 * (64 + dm));
     const float qn[4] = {(float)qn0[0], (float)qn0[1], (float)qn1[0], (float)qn1[1]};
     const float kn[4] = {(float)kn0[0], (float)kn0[1], (float)kn1[0], (float)kn1[1]};
     const float cs[4] = {(float)cv0[0], (float)cv0[1], (float)cv1[0], (float)cv1[1]};
@@ -860,35 +878,28 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
       *(h2*)(row + 64) = kv1;
     }
   }
-  // this wave's 16 positions: K lines 4c..4c+3, V lines nk + 4c ..
-  const int j = lane >> 4, q16 = lane & 15;
   // the scratch was written as fp16 vectors of another type: keep the compiler from
   // moving these reads above those writes (type-based alias analysis would allow it)
   asm volatile("" ::: "memory");
   const v4u qa = *(const v4u*)(qr + 8 * q16), qb = *(const v4u*)(qr + 128 + 8 * q16);  // q heads 0, 1 (fp16)
   // the current position is not in the cache lines (the loader reads a spare row for it):
-  // the wave whose 16 positions include it writes its fp16 k and v into its own ring lines
-  // (row jp of the line; all four rows of lanes write the same 16 bytes, so no lane branches)
+  // the wave whose 16 positions include it puts its fp16 k and v into row jp of its line
+  // registers (rows are lanes 16 jp .. 16 jp + 15)
   {
     const int mp = (pos - t0) >> 2, jp = (pos - t0) & 3;
     if (pos >= t0 && pos < t1 && (mp >> 2) == W.c) {
-      S->ring[(nkl + mp) % RING_LINES][16 * jp + q16] = *(const v4u*)(qr + 256 + 8 * q16);
-      S->ring[(nkl + nk + mp) % RING_LINES][16 * jp + q16] = *(const v4u*)(qr + 384 + 8 * q16);
+      const v4u kn = *(const v4u*)(qr + 256 + 8 * q16), vn = *(const v4u*)(qr + 384 + 8 * q16);
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb)
+        if (bb == (mp & 3) && j == jp) {
+          kw[bb] = kn;
+          vw[bb] = vn;
+        }
     }
   }
-  // all 8 K and V line reads are issued together: a wave whose lines run past the split's
-  // last (m >= nk) reads that last line again (or, for an empty split, the misc line),
-  // which holds finite values; those positions are masked out of the softmax
-  v4u kw[4], vw[4];
   bool valid[4];
 #pragma unroll
-  for (int bb = 0; bb < 4; ++bb) {
-    const int m = 4 * W.c + bb;
-    const int mm = nk > 0 ? min(m, nk - 1) : -LINES_ATTMISC;
-    valid[bb] = m < nk && t0 + 4 * m + j < t1;
-    kw[bb] = ring_ld(S, vbk, mm);
-    vw[bb] = ring_ld(S, vbk, (nk > 0 ? nk : 0) + mm);
-  }
+  for (int bb = 0; bb < 4; ++bb) valid[bb] = 4 * W.c + bb < nk && t0 + 4 * (4 * W.c + bb) + j < t1;
   float sc[4][2];
 #pragma unroll
   for (int bb = 0; bb < 4; ++bb) {
@@ -897,9 +908,6 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
     sc[bb][0] = valid[bb] ? s0 : -INFINITY;
     sc[bb][1] = valid[bb] ? s1 : -INFINITY;
   }
-  // the V lines are needed here at the latest: keeps their reads in the batch above
-#pragma unroll
-  for (int bb = 0; bb < 4; ++bb) asm volatile("" ::"v"(vw[bb]));
   float mh[2], lh[2], acc[2][8];
   float pr[2][4];
 #pragma unroll
