@@ -719,11 +719,7 @@ __device__ __forceinline__ void gain_act(const float (&xa)[8], const float (&xb)
   }
 }
 
-// one 2 KB weight row held in ring lines n, n + 1 dotted with (a | b)
-__device__ __forceinline__ float row2k(const Shared* S, u32 vb, int k, const float (&a)[8], const float (&b)[8]) {
-  return dot8(ring_ld(S, vb, k), a) + dot8(ring_ld(S, vb, k + 1), b);
-}
-// the same for a row already read from the ring into registers
+// one 2 KB weight row (read from ring lines n, n + 1 into registers) dotted with (a | b)
 __device__ __forceinline__ float row2k_r(const v4u& w0, const v4u& w1, const float (&a)[8], const float (&b)[8]) {
   return dot8(w0, a) + dot8(w1, b);
 }
@@ -740,7 +736,7 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   float xa[8], xb[8], ss;
   const u32 vb = ring_vbase(n0, lane);
   // the wave's ring lines (norm weights, 4 rows) are read into registers while it waits for
-  // its input, so no LDS latency follows the input's arrival
+  // its input, so no LDS latency follows the input's arrival, and released right away
   v4u wl[LINES_NORM + 8];
   auto lines = [&] {
     wait_lines(W, W.gl);
@@ -752,6 +748,7 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
       wl[LINES_NORM + 2 * r] = ring_ld(S, vb, LINES_NORM + 2 * (4 * W.c + r));
       wl[LINES_NORM + 2 * r + 1] = ring_ld(S, vb, LINES_NORM + 2 * (4 * W.c + r) + 1);
     }
+    release_lines(W, W.gl);
   };
   if (l == 0) {
     const _Float16* row = P.embed + (long)token * HIDDEN;
@@ -767,7 +764,6 @@ __device__ __forceinline__ void st_qkv(CW& W, const KParams& P, int t, int l, u3
   float part[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[r] = row2k_r(wl[LINES_NORM + 2 * r], wl[LINES_NORM + 2 * r + 1], a, b);
-  release_lines(W, W.gl);
   // lanes 0, 16, 32, 48 hold rows 0, 2, 1, 3
   const float rs = reduce4(part[0], part[1], part[2], part[3]) * rstd_of(ss);
   const float r0 = bcast(rs, 0), r1 = bcast(rs, 32), r2 = bcast(rs, 16), r3 = bcast(rs, 48);
@@ -799,8 +795,8 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
   // past the split's last (m >= nk) reads that last line again (or, for an empty split, the
   // misc line), which holds finite values; those positions are masked out of the softmax
   const int j = lane >> 4, q16 = lane & 15;
-  // the norm / cos / sin values and the wave's K and V lines are read into registers while
-  // the wave waits for its input
+  // the norm / cos / sin values and the wave's K and V lines are read into registers (and the
+  // lines released) while the wave waits for its input
   h2 qn0, qn1, kn0, kn1, cv0, cv1, sv0, sv1;
   v4u kw[4], vw[4];
   float2 qlo, qhi, klo, khi;
@@ -827,6 +823,7 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
         kw[bb] = ring_ld(S, vbk, mm);
         vw[bb] = ring_ld(S, vbk, (nk > 0 ? nk : 0) + mm);
       }
+      release_lines(W, W.gl);
     });
     *(float4*)(S->xs + 128 * W.c + 4 * (lane & 31)) =
         make_float4(lo_h(v[0].x), hi_h(v[0].x), lo_h(v[0].z), hi_h(v[0].z));
@@ -943,7 +940,6 @@ __device__ __forceinline__ void st_att(CW& W, const KParams& P, int t, int l, u3
 #pragma unroll
     for (int j = 0; j < 4; ++j) u[j] = pack16(tt[j], tt[j + 4]);
   }
-  release_lines(W, W.gl);
   float* rec = &S->apart[W.c][0][0];
   {
     const int R = lane >> 4;
@@ -1025,7 +1021,7 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   W.gl += LINES_O;
   v4u a;  // attention output values [8 (lane % 32), +8), fp16 as exchanged
   // line 4c + m holds rows 8c + 2m (lanes 0-31) and 8c + 2m + 1 (lanes 32-63); read into
-  // registers while the wave waits for its input
+  // registers (and released) while the wave waits for its input
   const u32 vb = ring_vbase(n0, lane);
   v4u wl[4];
   {
@@ -1037,6 +1033,7 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
       trace_ev(P, t, NSTAGE * l + S_O, TR_LINES);
 #pragma unroll
       for (int m = 0; m < 4; ++m) wl[m] = ring_ld(S, vb, 4 * W.c + m);
+      release_lines(W, W.gl);
     });
     a = v4u{v[0].x, v[0].z, v[1].x, v[1].z};
   }
@@ -1044,7 +1041,6 @@ __device__ __forceinline__ void st_o(CW& W, const KParams& P, int t, int l, u32 
   float part[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) part[m] = dot8h(wl[m], a);
-  release_lines(W, W.gl);
   // y0 rows: (line 0 lo, line 1 lo, line 0 hi, line 1 hi) = rows 8c + (0, 2, 1, 3); y1 = +4
   const float y0 = row16_sum(pack16(part[0], part[1])), y1 = row16_sum(pack16(part[2], part[3]));
   if ((lane & 15) == 0) {
@@ -1117,7 +1113,7 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
   const u32 vb = ring_vbase(n0, lane);
   constexpr int ng = LINES_NORM;
   // norm weights, then gate rows (wl[ng + 2 jj ..]) and up rows (wl[ng + 6 + 2 jj ..]),
-  // read into registers while the wave waits for its input
+  // read into registers (and released) while the wave waits for its input
   v4u wl[ng + 12];
   auto lines = [&] {
     wait_lines(W, W.gl);
@@ -1131,6 +1127,7 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
       wl[ng + 6 + 2 * jj] = ring_ld(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj));
       wl[ng + 6 + 2 * jj + 1] = ring_ld(S, vb, ng + 2 * GU_PER_WG + 2 * (3 * W.c + jj) + 1);
     }
+    release_lines(W, W.gl);
   };
   if (P.mode == MODE_MLP) {
     ss = load_x1024(P.in_vec, lane, xa, xb);
@@ -1148,7 +1145,6 @@ __device__ __forceinline__ void st_gu(CW& W, const KParams& P, int t, int l, u32
     part[jj] = row2k_r(wl[ng + 2 * jj], wl[ng + 2 * jj + 1], a, b);              // gate
     part[3 + jj] = row2k_r(wl[ng + 6 + 2 * jj], wl[ng + 6 + 2 * jj + 1], a, b);  // up
   }
-  release_lines(W, W.gl);
   float pq, qq;
   reduce6(part, pq, qq);  // pq rows: gate0, gate1, up0, up1; qq rows: gate2, gate2, up2, up2
   const float rstd = rstd_of(ss);
@@ -1176,7 +1172,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   W.gl += LINES_DOWN;
   v4u a;
   const u32 vb = ring_vbase(n0, lane);
-  v4u wl[8];  // the wave's 8 lines, read into registers while it waits for its input
+  v4u wl[8];  // the wave's 8 lines, read into registers (and released) while it waits for its input
   {
     // wave c polls slot pairs k = 32 c + lane (lanes < 32): workgroup k / 4, wave k % 4 ->
     // inter values 12 (k / 4) + 3 (k % 4) + {0, 1, 2} (the pair's last half is padding),
@@ -1189,6 +1185,7 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
       trace_ev(P, t, NSTAGE * l + S_DOWN, TR_LINES);
 #pragma unroll
       for (int r = 0; r < 8; ++r) wl[r] = ring_ld(S, vb, 8 * W.c + r);
+      release_lines(W, W.gl);
     });
     if (lane < 32) {
       const int k = 32 * W.c + lane;
@@ -1209,7 +1206,6 @@ __device__ __forceinline__ void st_down(CW& W, const KParams& P, int t, int l, u
   float part[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) part[r] = dot8h(wl[r], a);
-  release_lines(W, W.gl);
   float y0, y1;
   reduce8(part, y0, y1);
   if ((lane & 15) == 0) {
