@@ -1062,6 +1062,10 @@ __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u3
   const int st = is_down ? S_DSUM : S_OSUM;
   const int pr = lane & 3;  // rows 8 c + 2 pr, +1
   trace_ev(P, t, NSTAGE * l + st, TR_POLL);
+  // the input residual of the rows (this wave wrote it), read before the wait
+  float* res = is_down ? S->actres : S->resid;
+  float* out = is_down ? S->resid : S->actres;
+  const float2 rv = *(const float2*)(res + 8 * W.c + 2 * pr);
   float y0, y1;
   {  // lanes 0-31: XCD lane / 4, rows 8 c + 2 pr, +1
     const long src0 = xbuf(par, 0, is_down ? B_DP : B_OP) + HROWS * W.i + 8 * W.c;
@@ -1081,9 +1085,6 @@ __device__ __forceinline__ void st_sum(CW& W, const KParams& P, int t, int l, u3
   y1 = pack16(y1, y1);
   if (lane < 4) {
     const int r = 8 * W.c + 2 * pr;
-    float* res = is_down ? S->actres : S->resid;  // input residual
-    float* out = is_down ? S->resid : S->actres;
-    const float2 rv = *(const float2*)(res + r);
     const float s0 = y0 + rv.x, s1 = y1 + rv.y;
     *(float2*)(out + r) = make_float2(s0, s1);
     const int row = HROWS * W.i + r;
