@@ -139,7 +139,7 @@ def run_generate(args, n_prompt, n_new, name):
     return aux_line(f"batch-1 decode tokens/sec ({name}: {n_prompt}-id prompt, generate_nosync {n_new})",
                     round(n_new / ms * 1e3, 2), "tokens/s", True, name,
                     {"prompt": n_prompt, "new_tokens": n_new, "positions": f"{start}..{start + n_new - 1}"},
-                    "qwen_decode_kernel", algorithmic_bytes(start, n_new), ms, args.steps, args.warmup)
+                    "fast::qwen_decode_kernel", algorithmic_bytes(start, n_new), ms, args.steps, args.warmup)
 
 
 def run_lm_head(args):
@@ -168,7 +168,7 @@ def run_lm_head(args):
     ms = _median(ts)
     nbytes = 151936 * 1024 * 2 + 1024 * 2
     return aux_line("isolated lm_head + argmax (C1): microseconds per call", round(ms * 1e3, 2), "us/call",
-                    False, "c1", {"rows": 151936, "hidden": 1024, "copies": 2}, "qwen_decode_kernel",
+                    False, "c1", {"rows": 151936, "hidden": 1024, "copies": 2}, "fast::qwen_decode_kernel",
                     nbytes, ms, args.steps, args.warmup)
 
 
@@ -202,7 +202,7 @@ def run_mlp(args):
     ms = _median(ts)
     nbytes = 3 * 3072 * 1024 * 2 + 1024 * 2 + 2 * 1024 * 2
     return aux_line("isolated MLP block (C2): microseconds per call", round(ms * 1e3, 2), "us/call", False, "c2",
-                    {"hidden": 1024, "inter": 3072, "weight_sets": 16}, "qwen_decode_kernel", nbytes, ms,
+                    {"hidden": 1024, "inter": 3072, "weight_sets": 16}, "fast::qwen_decode_kernel", nbytes, ms,
                     args.steps, args.warmup)
 
 
@@ -331,7 +331,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
-            "kernel": "qwen_decode_kernel",
+            "kernel": "fast::qwen_decode_kernel",
             "bytes_per_launch": per_launch,
             "kernel_ms": round(avg_kernel_s * 1e3, 3),
         },
