@@ -160,7 +160,9 @@ int qwen_abi_version(void);
  * down, down sum; stage 8*num_layers is the lm_head input and argmax).
  * Events, all from compute wave 0 of the workgroup: 0 = starts waiting for the
  * stage input, 1 = has its quarter of the input, 2 = passed the compute-wave
- * barrier, 3 = stored its results. Pass buf = NULL to stop. */
+ * barrier, 3 = stored its results. Pass buf = NULL to stop. While tracing, the
+ * launches run a second build of the kernel that carries the trace points (a few
+ * microseconds per token slower); without it, the kernel has none. */
 int qwen_set_trace(unsigned long long* buf, int token);
 int qwen_trace_events(void);
 
