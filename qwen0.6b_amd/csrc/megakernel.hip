@@ -20,8 +20,11 @@
 //    never waits behind a prefetch;
 //  * waves 4-7 stream every stage's weights and K/V rows with LDS-DMA
 //    (global_load_lds_dwordx4) into a 128 KB ring of 1 KB lines, up to 128
-//    lines ahead of the compute waves; in the lm_head they compute rows
-//    alongside the compute waves;
+//    lines ahead of the compute waves; a compute wave reads its lines into
+//    registers (and frees them) while it waits for its input, so only the
+//    arithmetic follows the input's arrival. In the lm_head the loader waves
+//    compute rows alongside the compute waves, and the last fifth of the
+//    vocabulary is claimed at run time by groups of 8 workgroups (one per XCD);
 //  * the residual stream stays fp32 inside the workgroup that owns its rows;
 //    only the all-gathered copies are fp16;
 //  * every wait is bounded by a wall-clock deadline; a missed deadline sets a
