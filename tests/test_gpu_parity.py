@@ -258,6 +258,29 @@ def test_generate_until_stops_at_eos(ext, full, qa):
     assert ext.last_error() == 0
 
 
+def test_traced_kernel_matches_and_records(ext, full):
+    """The traced build of the kernel (launched while set_trace is on) gives the same
+    tokens as the production build and records, for the traced token, a wait start and
+    an acknowledged store (store >= start) for every stage of every workgroup."""
+    hw, w, packed = full
+    L = 2
+    ids = [11, 22, 33, 44, 55, 66]
+    ref, _, _ = Run(w, packed, L).forced(ext, ids, 0, logits=False, hidden=False)
+    fins = 8 * L + 1
+    ev = ext.trace_events()
+    buf = torch.zeros(256 * fins * ev, dtype=torch.int64, device="cuda")
+    ext.set_trace(buf, 3)
+    try:
+        got, _, _ = Run(w, packed, L).forced(ext, ids, 0, logits=False, hidden=False)
+    finally:
+        ext.set_trace(None, 0)
+    assert got == ref
+    tr = buf.view(256, fins, ev).cpu()[:, :8 * L]
+    assert bool((tr[..., 0] > 0).all()) and bool((tr[..., 3] > 0).all())
+    assert bool((tr[..., 3] >= tr[..., 0]).all())
+    assert ext.last_error() == 0
+
+
 def test_lm_head_argmax_1000_trials(ext, full):
     """Isolated lm_head + argmax: W = the seed-0 embedding [151936, 1024],
     h_t ~ N(0, 1) fp16 (PCG64 seed 1000 + t), 1000 trials."""
