@@ -61,6 +61,7 @@ typedef struct __attribute__((aligned(16))) LDGLayerWeight {
 #define QWEN_ERR_DEVICE 2     /* not a 256-CU gfx950 device, or no cooperative launch */
 #define QWEN_ERR_LAUNCH 3     /* HIP launch/allocation failure */
 #define QWEN_ERR_TIMEOUT 4    /* a device-side wait exceeded its deadline (reported by qwen_last_error) */
+#define QWEN_ERR_BAD_TOKEN 5  /* a teacher-forced id outside [0, 151936) reached the device (qwen_last_error) */
 
 /* One decode step at `position` (Tools/megakernel/megakernel.cu:1150-1196):
  * embedding of input_token_id, 28 layers writing K/V at `position`, final
@@ -76,7 +77,8 @@ int launch_ldg_decode_direct(
     float attn_scale, hipStream_t stream);
 
 /* Exported-but-unbound variant of the reference (megakernel.cu:1198-1244):
- * identical to launch_ldg_decode_direct; cache_len must be position + 1. */
+ * identical to launch_ldg_decode_direct. cache_len is accepted and not used, as
+ * in the reference, whose kernel attends over positions 0..position. */
 int launch_ldg_decode_persistent(
     int input_token_id, int* output_token_id, const void* embed_weight,
     const LDGLayerWeight* layer_weights, const void* final_norm_weight,
@@ -145,9 +147,19 @@ int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, const void* 
                    const void* up_weight, const void* down_weight, float* y_out, hipStream_t stream);
 
 /* Synchronizes the current device and returns the device-side error state of
- * the last launches (QWEN_OK or QWEN_ERR_TIMEOUT); clears it and resets the
- * workspace when set. */
+ * the last launches: QWEN_OK, QWEN_ERR_TIMEOUT (a wait exceeded its deadline)
+ * or QWEN_ERR_BAD_TOKEN (a forced id out of range); clears it and resets the
+ * workspace when set. (Workgroup placement, workgroup w on XCD w % 8, is checked
+ * once per device when the library first uses it: QWEN_ERR_DEVICE from every
+ * entry point if it does not hold.) */
 int qwen_last_error(void);
+
+/* Test hook (no counterpart in the reference): the wall-clock budget, in
+ * microseconds, of every single device-side wait of later launches on the
+ * current device; 0 restores the default (500000 us). A tiny budget makes the
+ * kernel's bounded waits give up, so the error path (status word, every wave
+ * leaving, qwen_last_error resetting the workspace) can be exercised. */
+int qwen_set_wait_deadline_us(long long us);
 
 /* 2 (QWEN_ABI_VERSION), as qwen_ops.cpp:30-32. */
 int qwen_abi_version(void);
@@ -155,7 +167,8 @@ int qwen_abi_version(void);
 /* Profiling aid: while buf is non-null, every launch on the current device
  * records wall-clock timestamps (s_memrealtime ticks, 100 MHz) for token index
  * `token` of the launch into buf[workgroup][stage][qwen_trace_events()]
- * (device u64, 256 x (8*num_layers+1) x events; stage 8*l + s is stage s of
+ * (device u64, 256 x (8*num_layers+1) x events, `elems` entries in all: a launch
+ * whose layers need more is refused with QWEN_ERR_ARG; stage 8*l + s is stage s of
  * layer l in the order QKV, attention, combine, o_proj, o_proj sum, gate/up,
  * down, down sum; stage 8*num_layers is the lm_head input and argmax).
  * Events, all from compute wave 0 of the workgroup: 0 = starts waiting for the
@@ -163,7 +176,7 @@ int qwen_abi_version(void);
  * barrier, 3 = stored its results. Pass buf = NULL to stop. While tracing, the
  * launches run a second build of the kernel that carries the trace points (a few
  * microseconds per token slower); without it, the kernel has none. */
-int qwen_set_trace(unsigned long long* buf, int token);
+int qwen_set_trace(unsigned long long* buf, long long elems, int token);
 int qwen_trace_events(void);
 
 #ifdef __cplusplus

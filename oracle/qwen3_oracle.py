@@ -30,9 +30,15 @@ Where the reference rounds intermediates to fp16 (s_norm, q/k/v, attn_out,
 the residual stream) this restatement keeps fp32: it is the fp32 reference
 the device path is measured against, with the tolerances stated in the tests.
 
-Pinned by tests/test_oracle.py: closed forms for every function below, and an
-end-to-end comparison with the third-party HuggingFace ``Qwen3ForCausalLM``
-(transformers, present in the image) on a small configuration.
+``Oracle.forward`` runs a whole id sequence at once (a causal prefill): the
+same per-position arithmetic as ``Oracle.step``, batched over positions, which
+is what the reference's prefill computes one ``step`` at a time
+(Model/Qwen06B_architecture.py:346-347).
+
+Pinned by tests/test_oracle.py: closed forms for every function below, float64
+brute force for the MLP block and the top-2 gap, and an end-to-end comparison
+with the third-party HuggingFace ``Qwen3ForCausalLM`` (transformers, present in
+the image) on a small configuration, for both ``step`` and ``forward``.
 """
 
 from __future__ import annotations
@@ -109,6 +115,8 @@ def argmax_lowest(logits: torch.Tensor) -> int:
 
 
 def top2_gap(logits: torch.Tensor) -> float:
+    """Largest logit minus the second largest (0 for an exact tie). Decides which
+    greedy steps are near-ties (gap < 1e-2) and exempt from the token check."""
     v = torch.topk(logits.float(), 2).values
     return float(v[0] - v[1])
 
@@ -126,6 +134,8 @@ class Oracle:
         self.shape = s
         f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).float()
         self.embed = f32(hw.embed)
+        lm = getattr(hw, "lm_head", None)
+        self.lm_head = self.embed if lm is None else f32(lm)
         self.layers = [[f32(t) for t in layer] for layer in hw.layers]
         self.final_norm = f32(hw.final_norm)
         if rope == "fp16":
@@ -169,8 +179,53 @@ class Oracle:
         if not want_logits:
             return dict(hidden=x)
         norm_out = rms_norm(x, self.final_norm)
-        logits = lm_head_logits(self.embed, norm_out)
+        logits = lm_head_logits(self.lm_head, norm_out)
         return dict(logits=logits, hidden=x, norm_out=norm_out, token=argmax_lowest(logits))
+
+    @torch.no_grad()
+    def forward(self, ids: list, start: int = 0, logits_at=()) -> dict:
+        """Causal forward of ``ids`` at positions ``start .. start + n - 1`` in one batch
+        (every position attends to the cache at positions ``< start`` and to the ids
+        before it). Writes K/V at those positions, as ``n`` calls of ``step`` would.
+
+        Returns ``hidden`` [n, H] (each position's final-layer residual before the final
+        norm) and, for the positions listed in ``logits_at``, ``logits`` [m, V],
+        ``norm_out`` [m, H] and the greedy ``tokens``."""
+        s = self.shape
+        n = len(ids)
+        assert n >= 1 and start >= 0 and start + n <= s.max_seq
+        pos = torch.arange(start, start + n)
+        x = self.embed[torch.tensor(ids, dtype=torch.long)].clone()  # [n, H]
+        cos, sin = self.cos[pos][:, None, :], self.sin[pos][:, None, :]  # [n, 1, D]
+        total = start + n
+        # query i (position start + i) sees keys 0 .. start + i
+        mask = torch.arange(total)[None, :] > pos[:, None]  # [n, total]
+        group = s.q_heads // s.kv_heads
+        for li, (w_in, wq, wk, wv, w_qn, w_kn, wo, w_post, wg, wu, wd) in enumerate(self.layers):
+            h = rms_norm(x, w_in)
+            q = (h @ wq.T).view(n, s.q_heads, s.head_dim)
+            k = (h @ wk.T).view(n, s.kv_heads, s.head_dim)
+            v = (h @ wv.T).view(n, s.kv_heads, s.head_dim)
+            q = apply_rope(rms_norm(q, w_qn), cos, sin)
+            k = apply_rope(rms_norm(k, w_kn), cos, sin)
+            self.k_cache[li, :, start:total] = k.transpose(0, 1)
+            self.v_cache[li, :, start:total] = v.transpose(0, 1)
+            kk = self.k_cache[li, :, :total].repeat_interleave(group, dim=0)  # [Hq, total, D]
+            vv = self.v_cache[li, :, :total].repeat_interleave(group, dim=0)
+            sc = torch.matmul(q.transpose(0, 1), kk.transpose(1, 2)) * self.scale  # [Hq, n, total]
+            sc = sc.masked_fill(mask[None], float("-inf"))
+            attn = torch.matmul(torch.softmax(sc, dim=-1), vv)  # [Hq, n, D]
+            x = x + attn.transpose(0, 1).reshape(n, s.q_size) @ wo.T
+            hh = rms_norm(x, w_post)
+            x = x + (torch.nn.functional.silu(hh @ wg.T) * (hh @ wu.T)) @ wd.T
+        out = dict(hidden=x)
+        idx = [int(p) - start for p in logits_at]
+        if idx:
+            assert all(0 <= i < n for i in idx)
+            norm_out = rms_norm(x[idx], self.final_norm)
+            logits = norm_out @ self.lm_head.T
+            out.update(norm_out=norm_out, logits=logits, tokens=[argmax_lowest(r) for r in logits])
+        return out
 
     def greedy(self, prompt: list, n_new: int, start: int = 0) -> dict:
         """Prefill ``prompt[:-1]`` step by step, then ``n_new`` greedy steps

@@ -100,14 +100,21 @@ def _synchronize() -> None:
         torch.cuda.synchronize()
 
 
+_DEVICE_ERRORS = {
+    4: "a cross-workgroup wait exceeded its deadline",
+    5: "a forced token id outside the vocabulary reached the device",
+}
+
+
 def _check_device_errors() -> None:
     fn = getattr(qwen_megakernel_C, "last_error", None)
     if fn is None:
         return
     rc = int(fn())
     if rc != 0:
+        why = _DEVICE_ERRORS.get(rc, "unknown error")
         raise RuntimeError(
-            f"qwen_megakernel_C device-side error {rc}: a cross-workgroup wait exceeded its deadline "
+            f"qwen_megakernel_C device-side error {rc}: {why} "
             "(the engine state was reset; call Decoder.reset() before continuing)"
         )
 

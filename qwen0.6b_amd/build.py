@@ -6,13 +6,23 @@ Produces, next to this file:
   layout_check                           host-side exhaustive index checker (run here)
 
 All HIP code is compiled with ``-Xclang -target-feature -Xclang -packed-fp32-ops``
-(packed fp32 instructions disabled).
+(packed fp32 instructions disabled). hipcc passes the flag to both of its
+compiler passes; the x86 host pass prints "'-packed-fp32-ops' is not a
+recognized feature for this target (ignoring feature)", the gfx950 device pass
+applies it. ``audit_device_code`` enforces the result on every build: it reads
+the gfx950 code object out of the built library, disassembles it and fails the
+build if it holds a packed fp32 add, multiply or fma, or any use of ``m0`` other
+than the ``s_mov_b32 m0`` that directly precedes each LDS-DMA load (the one
+inline-asm sequence that sets it; hipcc warns about that clobber).
 """
 
 import os
+import re
+import struct
 import subprocess
 import sys
 import sysconfig
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
@@ -38,7 +48,52 @@ def build_kernels():
     out = os.path.join(HERE, "libqwen_megakernel.so")
     _run([HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared", f"-I{INC}", f"-I{CSRC}",
           *NO_PACKED_FP32, *NO_SINK, os.path.join(CSRC, "megakernel.hip"), "-o", out])
+    audit_device_code(out)
     return out
+
+
+def device_code_object(lib):
+    """The gfx950 code object inside a hipcc-built shared library (an uncompressed
+    clang offload bundle: 24-byte magic, entry count, then offset/size/triple per entry)."""
+    data = open(lib, "rb").read()
+    base = data.find(b"__CLANG_OFFLOAD_BUNDLE__")
+    if base < 0:
+        raise RuntimeError(f"{lib}: no offload bundle found")
+    (n,) = struct.unpack_from("<Q", data, base + 24)
+    o = base + 32
+    for _ in range(n):
+        off, size, tlen = struct.unpack_from("<QQQ", data, o)
+        o += 24
+        triple = data[o:o + tlen].decode()
+        o += tlen
+        if triple.endswith(ARCH):
+            return data[base + off:base + off + size]
+    raise RuntimeError(f"{lib}: no {ARCH} code object in the bundle")
+
+
+def audit_device_code(lib):
+    """Disassemble the library's gfx950 code and check two build invariants."""
+    objdump = os.path.join(os.path.dirname(os.path.realpath(HIPCC)), "..", "llvm", "bin", "llvm-objdump")
+    if not os.path.exists(objdump):
+        objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    with tempfile.TemporaryDirectory() as td:
+        co = os.path.join(td, "kernel.co")
+        with open(co, "wb") as f:
+            f.write(device_code_object(lib))
+        dis = subprocess.run([objdump, "-d", f"--mcpu={ARCH}", co], check=True, capture_output=True, text=True).stdout
+    ins = [ln.split("//")[0].strip() for ln in dis.splitlines() if ln[:1] in ("\t", " ")]
+    ins = [x for x in ins if x]
+    packed = [x for x in ins if re.match(r"v_pk_(add|mul|fma)_f32\b", x)]
+    if packed:
+        raise RuntimeError(f"{lib}: {len(packed)} packed fp32 instructions, e.g. {packed[0]}")
+    m0_uses = [k for k, x in enumerate(ins) if re.search(r"\bm0\b", x)]
+    bad = [ins[k] for k in m0_uses
+           if not (ins[k].startswith("s_mov_b32 m0,") and k + 1 < len(ins)
+                   and ins[k + 1].startswith("global_load_lds_dwordx4"))]
+    if bad:
+        raise RuntimeError(f"{lib}: m0 used outside the LDS-DMA sequence: {bad[:3]}")
+    print(f"device code audit: {len(ins)} instructions, no packed fp32, m0 set only before "
+          f"{len(m0_uses)} LDS-DMA loads", flush=True)
 
 
 def build_layout_check():

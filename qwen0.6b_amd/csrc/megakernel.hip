@@ -39,6 +39,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 
@@ -57,6 +58,8 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 constexpr float RMS_EPS = 1e-6f;
 constexpr u32 ST_TIMEOUT = 1u;
 constexpr u32 ST_BAD_TOKEN = 2u;
+// XCC id of the executing wave: s_getreg of hardware register 20 (XCC_ID), bits [3:0]
+__device__ __forceinline__ u32 xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20); }
 constexpr int DMA_DEPTH = 16;  // LDS-DMA lines a loader wave keeps in flight
 // optional device timestamps (wall clock) per workgroup and stage of one token
 constexpr int TRACE_EVENTS = 6;
@@ -115,26 +118,68 @@ constexpr bool kTrace = true;
 #include "decode_body.inc"
 }  // namespace traced
 
+// one workgroup per CU, as the decode kernel: each records the XCC it runs on
+__global__ void __launch_bounds__(BLOCK, 1) qwen_placement_probe(u32* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
 // ------------------------------------------------------------------------------------
 // host side
 
 namespace {
 
 constexpr int MAX_DEVICES = 16;
+constexpr u64 DEFAULT_WAIT_US = 500000;
 
 struct DeviceState {
   bool init = false;
   int err = QWEN_OK;
   u64* ws = nullptr;
   u32* status = nullptr;
+  LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
   u32 epoch = 1;
+  u64 clk_khz = 100000;
   u64 deadline = 0;
   u64* trace = nullptr;
+  long long trace_elems = 0;
   int trace_token = -1;
 };
 
 std::mutex g_mu;
 DeviceState g_dev[MAX_DEVICES];
+std::once_flag g_teardown_once;
+
+// At process exit, before the HIP runtime's own teardown (registered earlier, so run
+// later): wait for the device and free what the library allocated.
+void teardown() {
+  std::lock_guard<std::mutex> lock(g_mu);
+  for (int d = 0; d < MAX_DEVICES; ++d) {
+    DeviceState& st = g_dev[d];
+    if (!st.ws && !st.tab) continue;
+    if (hipSetDevice(d) != hipSuccess) continue;
+    (void)hipDeviceSynchronize();
+    if (st.ws) (void)hipFree(st.ws);
+    if (st.tab) (void)hipFree(st.tab);
+    st = DeviceState();
+  }
+}
+
+// Every workgroup w of a 256 x 512 launch must run on XCD w % 8: the work partition and the
+// XCD-local exchange stores rely on it. Checked once per device with a probe launch.
+int check_placement(u32* scratch, hipStream_t s) {
+  void* args[] = {&scratch};
+  if (hipLaunchCooperativeKernel((const void*)qwen_placement_probe, dim3(NWG), dim3(BLOCK), args, 0, s) != hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  u32 xcc[NWG];
+  if (hipMemcpy(xcc, scratch, sizeof(xcc), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
+  for (int w = 0; w < NWG; ++w)
+    if ((int)(xcc[w] & 15) != xcd_of(w)) {
+      fprintf(stderr, "qwen_megakernel: workgroup %d runs on XCC %u, the work partition needs XCC %d\n", w,
+              xcc[w] & 15, xcd_of(w));
+      return QWEN_ERR_DEVICE;
+    }
+  return QWEN_OK;
+}
 
 int device_state(DeviceState** out) {
   int dev = 0;
@@ -164,11 +209,19 @@ int device_state(DeviceState** out) {
     int clk_khz = 0;
     if (hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || clk_khz <= 0)
       clk_khz = 100000;
-    st.deadline = (u64)clk_khz * 500;  // 0.5 s per single wait
+    st.clk_khz = (u64)clk_khz;
+    st.deadline = st.clk_khz * DEFAULT_WAIT_US / 1000;  // 0.5 s per single wait
     void* p = nullptr;
     if (hipMalloc(&p, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-    if (hipMemset(p, 0, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+    std::call_once(g_teardown_once, [] { std::atexit(teardown); });
     st.ws = (u64*)p;
+    const int pc = check_placement((u32*)p, nullptr);
+    if (pc != QWEN_OK) {
+      st.err = pc;
+      st.init = true;
+      return st.err;
+    }
+    if (hipMemset(p, 0, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
     st.status = (u32*)((char*)p + TOTAL_SLOTS * 8);
     st.init = true;
   }
@@ -182,6 +235,8 @@ int launch(KParams& P, hipStream_t stream) {
   DeviceState* st = nullptr;
   int rc = device_state(&st);
   if (rc != QWEN_OK) return rc;
+  // a trace buffer must hold every stage of every workgroup of this launch's layers
+  if (st->trace && (long long)NWG * trace_stages(P.num_layers) * TRACE_EVENTS > st->trace_elems) return QWEN_ERR_ARG;
   P.ws = st->ws;
   P.status = st->status;
   P.deadline = st->deadline;
@@ -264,7 +319,7 @@ extern "C" int launch_ldg_decode_persistent(int input_token_id, int* output_toke
                                             void* c, void* d, void* e, void* f, void* g, void* g_normalized, void* h,
                                             void* i, int num_layers, int position, int cache_len, int max_seq_len,
                                             float attn_scale, hipStream_t stream) {
-  if (cache_len != position + 1) return QWEN_ERR_ARG;
+  (void)cache_len;  // unused by the reference too: its kernel reads the position (megakernel.cu:1211-1230)
   return launch_ldg_decode_direct(input_token_id, output_token_id, embed_weight, layer_weights, final_norm_weight,
                                   lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, a, b, c, d,
                                   e, f, g, g_normalized, h, i, num_layers, position, max_seq_len, attn_scale, stream);
@@ -349,25 +404,27 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
       !aligned16(down_weight) || !aligned16(y_out))
     return QWEN_ERR_ARG;
   // the kernel reads the layer pointer table from device memory
-  static LDGLayerWeight* d_tab[MAX_DEVICES] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return QWEN_ERR_DEVICE;
   LDGLayerWeight h;
   memset(&h, 0, sizeof(h));
   h.post_attn_layernorm_weight = post_norm_weight;
   h.gate_proj_weight = gate_weight;
   h.up_proj_weight = up_weight;
   h.down_proj_weight = down_weight;
+  LDGLayerWeight* tab = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_mu);
-    if (!d_tab[dev] && hipMalloc(&d_tab[dev], sizeof(LDGLayerWeight)) != hipSuccess) return QWEN_ERR_LAUNCH;
+    DeviceState* st = nullptr;
+    int rc = device_state(&st);
+    if (rc != QWEN_OK) return rc;
+    if (!st->tab && hipMalloc(&st->tab, sizeof(LDGLayerWeight)) != hipSuccess) return QWEN_ERR_LAUNCH;
+    tab = st->tab;
   }
-  if (hipMemcpyAsync(d_tab[dev], &h, sizeof(h), hipMemcpyHostToDevice, stream) != hipSuccess) return QWEN_ERR_LAUNCH;
+  if (hipMemcpyAsync(tab, &h, sizeof(h), hipMemcpyHostToDevice, stream) != hipSuccess) return QWEN_ERR_LAUNCH;
   if (hipStreamSynchronize(stream) != hipSuccess) return QWEN_ERR_LAUNCH;
   KParams P;
   memset(&P, 0, sizeof(P));
   P.eos = -1;
-  P.layers = d_tab[dev];
+  P.layers = tab;
   P.in_vec = (const _Float16*)x_f16;
   P.out_vec = y_out;
   P.mode = MODE_MLP;
@@ -391,17 +448,31 @@ extern "C" int qwen_last_error(void) {
   // a failed launch leaves slots in an unknown state: start clean
   if (hipMemset(st.ws, 0, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
   st.epoch = 1;
+  if (s & ST_BAD_TOKEN) return QWEN_ERR_BAD_TOKEN;
   return QWEN_ERR_TIMEOUT;
+}
+
+extern "C" int qwen_set_wait_deadline_us(long long us) {
+  if (us < 0) return QWEN_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceState* st = nullptr;
+  int rc = device_state(&st);
+  if (rc != QWEN_OK) return rc;
+  st->deadline = st->clk_khz * (us == 0 ? DEFAULT_WAIT_US : (u64)us) / 1000;
+  if (st->deadline == 0) st->deadline = 1;
+  return QWEN_OK;
 }
 
 extern "C" int qwen_abi_version(void) { return QWEN_ABI_VERSION; }
 
-extern "C" int qwen_set_trace(unsigned long long* buf, int token) {
+extern "C" int qwen_set_trace(unsigned long long* buf, long long elems, int token) {
+  if (buf && elems <= 0) return QWEN_ERR_ARG;
   std::lock_guard<std::mutex> lock(g_mu);
   DeviceState* st = nullptr;
   int rc = device_state(&st);
   if (rc != QWEN_OK) return rc;
   st->trace = buf;
+  st->trace_elems = buf ? elems : 0;
   st->trace_token = buf ? token : -1;
   return QWEN_OK;
 }

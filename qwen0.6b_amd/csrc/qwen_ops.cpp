@@ -32,10 +32,12 @@ hipStream_t stream_of(const torch::Tensor& t) { return c10::hip::getCurrentHIPSt
 
 void check_rc(int rc, const char* what) {
   if (rc == QWEN_OK) return;
-  const char* why = rc == QWEN_ERR_ARG      ? "invalid argument"
-                    : rc == QWEN_ERR_DEVICE ? "unsupported device (needs a 256-CU gfx950 MI355X with cooperative launch)"
-                    : rc == QWEN_ERR_LAUNCH ? "HIP launch or allocation failure"
-                                            : "device-side timeout";
+  const char* why = rc == QWEN_ERR_ARG         ? "invalid argument"
+                    : rc == QWEN_ERR_DEVICE    ? "unsupported device (needs a 256-CU gfx950 MI355X with cooperative "
+                                                 "launch and workgroup w on XCD w % 8)"
+                    : rc == QWEN_ERR_LAUNCH    ? "HIP launch or allocation failure"
+                    : rc == QWEN_ERR_BAD_TOKEN ? "a forced token id out of range reached the device"
+                                               : "device-side timeout";
   TORCH_CHECK(false, "qwen_megakernel_C.", what, " failed: ", why, " (code ", rc, ")");
 }
 
@@ -218,13 +220,17 @@ int last_error() { return qwen_last_error(); }
 
 void set_trace(c10::optional<torch::Tensor> buf, int token) {
   if (!buf.has_value()) {
-    check_rc(qwen_set_trace(nullptr, -1), "set_trace");
+    check_rc(qwen_set_trace(nullptr, 0, -1), "set_trace");
     return;
   }
   TORCH_CHECK(buf->is_cuda() && buf->scalar_type() == torch::kLong && buf->is_contiguous(),
               "trace buffer must be a contiguous int64 GPU tensor");
-  check_rc(qwen_set_trace(reinterpret_cast<unsigned long long*>(buf->data_ptr<int64_t>()), token), "set_trace");
+  TORCH_CHECK(buf->numel() > 0, "trace buffer is empty");
+  check_rc(qwen_set_trace(reinterpret_cast<unsigned long long*>(buf->data_ptr<int64_t>()), buf->numel(), token),
+           "set_trace");
 }
+
+void set_wait_deadline_us(int64_t us) { check_rc(qwen_set_wait_deadline_us(us), "set_wait_deadline_us"); }
 
 }  // namespace
 
@@ -254,4 +260,6 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
   m.def("set_trace", &set_trace, "record per-stage device timestamps of one token into an int64 GPU tensor "
         "[256, fins, events] (None to stop)", pybind11::arg("buf"), pybind11::arg("token") = 0);
   m.def("trace_events", &qwen_trace_events, "events recorded per stage by set_trace");
+  m.def("set_wait_deadline_us", &set_wait_deadline_us, "test hook: wall-clock budget of every device-side wait "
+        "of later launches (0 = default 0.5 s)");
 }

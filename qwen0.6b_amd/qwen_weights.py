@@ -14,7 +14,13 @@ same fp16 values:
 * tensor ids: 0 = embedding, ``1 + 11*layer + field`` for the per-layer fields;
   the embedding is drawn in blocks of ``EMBED_BLOCK_ROWS`` rows, block ``c``
   from ``SeedSequence([seed, 0, c + 1])``, so it can be drawn in parallel;
-* RMSNorm weights (fields 0, 4, 5, 7 and the final norm) are all 1.0.
+* RMSNorm weights (fields 0, 4, 5, 7 and the final norm) are all 1.0 with
+  ``norms="ones"`` (the default workload); with ``norms="random"`` each is
+  ``1 + 0.5 * N(0, 1)`` from its own stream (tensor id of its field; the final
+  norm is id ``1 + 11 * layers``), so every layer and every field differs, as
+  real checkpoints do;
+* ``untied=True`` adds a separate lm_head matrix (``N(0, std)``, tensor id
+  ``(0, 0)``) in place of the tied embedding.
 
 The RoPE tables follow Model/Qwen06B_architecture.py:134-142: ``inv_freq`` and
 the angle table are built in fp32, ``cos``/``sin`` are taken in fp32, repeated
@@ -114,6 +120,11 @@ class HostWeights:
     final_norm: np.ndarray = None
     cos: np.ndarray = None
     sin: np.ndarray = None
+    lm_head: np.ndarray = None  # None: tied to the embedding (Model/Qwen06B_architecture.py:167)
+
+    @property
+    def lm_head_or_embed(self) -> np.ndarray:
+        return self.embed if self.lm_head is None else self.lm_head
 
     def digest(self) -> str:
         """sha256 over every tensor's fp16 bytes in tensor-id order."""
@@ -123,14 +134,28 @@ class HostWeights:
             for t in layer:
                 h.update(np.ascontiguousarray(t).view(np.uint16).tobytes())
         h.update(np.ascontiguousarray(self.final_norm).view(np.uint16).tobytes())
+        if self.lm_head is not None:
+            h.update(np.ascontiguousarray(self.lm_head).view(np.uint16).tobytes())
         return h.hexdigest()
 
 
-def host_weights(seed: int = 0, std: float = 0.02, shape: QwenShape = QWEN3_0_6B) -> HostWeights:
-    """Draw one synthetic model into host fp16 arrays."""
+def _norm_fp16(seed, tensor_id, shape: tuple) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(np.random.SeedSequence([seed, tensor_id])))
+    x = rng.standard_normal(int(np.prod(shape)), dtype=np.float32)
+    return (np.float32(1.0) + np.float32(0.5) * x).astype(np.float16).reshape(shape)
+
+
+def host_weights(seed: int = 0, std: float = 0.02, shape: QwenShape = QWEN3_0_6B, norms: str = "ones",
+                 untied: bool = False) -> HostWeights:
+    """Draw one synthetic model into host fp16 arrays (``norms``: "ones" or "random")."""
+    if norms not in ("ones", "random"):
+        raise ValueError(f"norms must be 'ones' or 'random', not {norms!r}")
     jobs = []
     for c, r0 in enumerate(range(0, shape.vocab, EMBED_BLOCK_ROWS)):
         jobs.append(((0, c + 1), (min(EMBED_BLOCK_ROWS, shape.vocab - r0), shape.hidden)))
+    if untied:
+        for c, r0 in enumerate(range(0, shape.vocab, EMBED_BLOCK_ROWS)):
+            jobs.append(((0, 0, c + 1), (min(EMBED_BLOCK_ROWS, shape.vocab - r0), shape.hidden)))
     for layer in range(shape.layers):
         for f in range(len(LAYER_FIELDS)):
             if f not in NORM_FIELDS:
@@ -138,14 +163,20 @@ def host_weights(seed: int = 0, std: float = 0.02, shape: QwenShape = QWEN3_0_6B
     # Each tensor has its own stream, so drawing them concurrently is deterministic.
     with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
         drawn = dict(zip([j[0] for j in jobs], ex.map(lambda j: _normal_fp16(seed, j[0], j[1], std), jobs)))
-    embed = np.concatenate([drawn[(0, c + 1)] for c in range((shape.vocab + EMBED_BLOCK_ROWS - 1) // EMBED_BLOCK_ROWS)])
+    nblk = (shape.vocab + EMBED_BLOCK_ROWS - 1) // EMBED_BLOCK_ROWS
+    embed = np.concatenate([drawn[(0, c + 1)] for c in range(nblk)])
+    lm_head = np.concatenate([drawn[(0, 0, c + 1)] for c in range(nblk)]) if untied else None
+
+    def norm(tensor_id, shp):
+        return np.ones(shp, dtype=np.float16) if norms == "ones" else _norm_fp16(seed, tensor_id, shp)
+
     layers = []
     for layer in range(shape.layers):
         fields = []
         for f in range(len(LAYER_FIELDS)):
             shp = shape.field_shape(f)
             if f in NORM_FIELDS:
-                fields.append(np.ones(shp, dtype=np.float16))
+                fields.append(norm(1 + 11 * layer + f, shp))
             else:
                 fields.append(drawn[1 + 11 * layer + f])
         layers.append(fields)
@@ -154,9 +185,10 @@ def host_weights(seed: int = 0, std: float = 0.02, shape: QwenShape = QWEN3_0_6B
         shape=shape,
         embed=embed,
         layers=layers,
-        final_norm=np.ones((shape.hidden,), dtype=np.float16),
+        final_norm=norm(1 + 11 * shape.layers, (shape.hidden,)),
         cos=cos.numpy(),
         sin=sin.numpy(),
+        lm_head=lm_head,
     )
 
 
@@ -179,6 +211,7 @@ def device_weights(hw: HostWeights, device: str = "cuda") -> dict:
         return torch.from_numpy(np.ascontiguousarray(a)).to(device)
 
     embed = up(hw.embed)
+    lm_head = embed if hw.lm_head is None else up(hw.lm_head)
     layer_weights = []
     for layer in hw.layers:
         for t in layer:
@@ -187,7 +220,7 @@ def device_weights(hw: HostWeights, device: str = "cuda") -> dict:
         embed_weight=embed,
         layer_weights=layer_weights,
         final_norm_weight=up(hw.final_norm),
-        lm_head_weight=embed,  # tied embeddings (Model/Qwen06B_architecture.py:167)
+        lm_head_weight=lm_head,  # tied unless the model has its own (Model/Qwen06B_architecture.py:167)
         cos_table=up(hw.cos),
         sin_table=up(hw.sin),
     )

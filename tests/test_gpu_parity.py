@@ -7,11 +7,17 @@ Tolerances (stated by the engine's contract):
   * logits max-abs error <= 5e-2;
   * isolated MLP block max-abs error <= 1e-2;
   * isolated lm_head argmax exact except where the top-2 gap < 1e-2.
-All inputs are seeded (weights N(0, 0.02) seed 0, norms 1.0; prompts PCG64).
-Every call goes through qwen_megakernel_C -> libqwen_megakernel.so.
+All inputs are seeded (weights N(0, 0.02) seed 0; prompts PCG64). The default
+model has unit RMSNorm weights and a tied lm_head, as the benchmark workload;
+the ``rn`` model has norm weights 1 + 0.5 N(0, 1), distinct for every layer and
+field, and its own lm_head matrix, so a dropped or misrouted norm gain or an
+lm_head read from the embedding fails. Every call goes through
+qwen_megakernel_C -> libqwen_megakernel.so (or the C-ABI directly via ctypes).
 """
 
+import ctypes
 import math
+import os
 
 import numpy as np
 import pytest
@@ -49,6 +55,16 @@ def qa():
 def full(qa):
     hw = qw.host_weights(seed=0, std=0.02)
     w = qw.device_weights(hw, "cuda")
+    packed = qa._pack_layer_weights(w["layer_weights"])
+    return hw, w, packed
+
+
+@pytest.fixture(scope="module")
+def rn(qa):
+    """Non-unit norms (distinct per layer and field) and an untied lm_head."""
+    hw = qw.host_weights(seed=0, std=0.02, norms="random", untied=True)
+    w = qw.device_weights(hw, "cuda")
+    assert w["lm_head_weight"].data_ptr() != w["embed_weight"].data_ptr()
     packed = qa._pack_layer_weights(w["layer_weights"])
     return hw, w, packed
 
@@ -120,6 +136,149 @@ def test_full_model_teacher_forced_matches_oracle(ext, full):
     last = ref["steps"][-1]
     assert float((run.hidden.float().cpu() - last["hidden"]).abs().max()) <= TOL_HIDDEN
     assert float((run.norm_out.cpu() - last["norm_out"]).abs().max()) <= 5e-2
+
+
+def test_random_norms_untied_lm_head_teacher_forced(ext, rn):
+    """The C0 workload on the rn model: 16-id prompt + 32 teacher-forced greedy steps,
+    28 layers: tokens, logits, hidden state, K/V cache and norm_out. Every RMSNorm gain
+    (input, post-attention, q_norm, k_norm, final) differs from 1 and between layers and
+    fields, and the lm_head is not the embedding."""
+    hw, w, packed = rn
+    # the fields really differ, so a swapped pair changes the result
+    assert not np.array_equal(hw.layers[0][4], hw.layers[0][5])
+    assert not np.array_equal(hw.layers[0][0], hw.layers[0][7])
+    assert not np.array_equal(hw.layers[0][0], hw.layers[1][0])
+    prompt = qw.synthetic_prompt(16, seed=1)
+    oracle = orc.Oracle(hw)
+    ref = oracle.greedy(prompt, 32)
+    ids = prompt + ref["tokens"][:-1]
+    run = Run(w, packed, 28)
+    toks, logits, hidden = run.forced(ext, ids, 0)
+    _compare_steps(ref["steps"], toks, logits, hidden, len(prompt) - 1, "rn c0")
+    kc = run.kc[:, :, : len(ids)].float().cpu()
+    vc = run.vc[:, :, : len(ids)].float().cpu()
+    dk = float((kc - oracle.k_cache[:, :, : len(ids)]).abs().max())
+    dv = float((vc - oracle.v_cache[:, :, : len(ids)]).abs().max())
+    print(f"rn c0: K max-abs {dk:.3e}, V max-abs {dv:.3e}")
+    assert dk < 2e-2 and dv < 2e-2
+    last = ref["steps"][-1]
+    assert float((run.hidden.float().cpu() - last["hidden"]).abs().max()) <= TOL_HIDDEN
+    assert float((run.norm_out.cpu() - last["norm_out"]).abs().max()) <= 5e-2
+
+
+def test_c4_full_size_prefill1920_generate128(ext, full, qa):
+    """C4 at full size: 28 layers, a 1920-id prompt (seed 1) prefilled, then one
+    generate_nosync launch of 128 tokens at positions 1920..2047 (context up to 2048),
+    as the benchmark runs it. The oracle runs one batched causal forward over the
+    engine's own 2048 inputs, so every one of the 129 greedy choices (the prefill's and
+    the 128 generated) is checked (near-ties exempt); logits and hidden states are
+    compared at every 8th of those positions and the K/V cache at all 2048."""
+    hw, w, packed = full
+    prompt = qw.synthetic_prompt(1921, seed=1)
+    dec = qa.Decoder(weights=w, verbose=False)
+    first = dec.prefill(prompt[:1920])
+    gen = dec.generate_nosync(first, 128).cpu().tolist()
+    qa._check_device_errors()
+    assert dec.position == 2048
+    ids = prompt[:1920] + [first] + gen[:-1]
+    got = [first] + gen  # argmax at positions 1919 .. 2047
+    at = list(range(1919, 2048))
+    oracle = orc.Oracle(hw)
+    ref = oracle.forward(ids, logits_at=at)
+    exempt = 0
+    for j, p in enumerate(at):
+        gap = orc.top2_gap(ref["logits"][j])
+        if gap >= GAP_EXEMPT:
+            assert got[j] == ref["tokens"][j], f"c4 position {p}: token {got[j]} != {ref['tokens'][j]}"
+        else:
+            exempt += 1
+    kc = dec._k_cache.float().cpu()
+    vc = dec._v_cache.float().cpu()
+    dk = float((kc - oracle.k_cache).abs().max())
+    dv = float((vc - oracle.v_cache).abs().max())
+    assert dk < 2e-2 and dv < 2e-2, (dk, dv)
+    # the same ids teacher forced through generate_ex: identical tokens, and logits / hidden
+    run = Run(w, packed, 28)
+    run.forced(ext, ids[:1919], 0, logits=False, hidden=False)
+    toks, logits, hidden = run.forced(ext, ids[1919:], 1919)
+    assert toks == got, "teacher-forced run differs from prefill + generate_nosync"
+    worst_l = worst_h = 0.0
+    for j in list(range(0, len(at), 8)) + [len(at) - 1]:
+        dl = float((logits[j] - ref["logits"][j]).abs().max())
+        dh = float((hidden[j] - ref["hidden"][at[j]]).abs().max())
+        worst_l, worst_h = max(worst_l, dl), max(worst_h, dh)
+        assert dl <= TOL_LOGITS, f"c4 position {at[j]}: logits max-abs {dl}"
+        assert dh <= TOL_HIDDEN, f"c4 position {at[j]}: hidden max-abs {dh}"
+    print(f"c4: 129 greedy choices checked ({exempt} near-tie exempt); worst logits {worst_l:.3e}, "
+          f"hidden {worst_h:.3e}; K/V cache max-abs {dk:.3e} / {dv:.3e}")
+
+
+def _lib():
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "qwen0.6b_amd",
+                                   "libqwen_megakernel.so"))
+    return lib
+
+
+def test_decode_persistent_c_abi(ext, full, qa):
+    """launch_ldg_decode_persistent through the C-ABI (ctypes, the reference's 27-argument
+    order with cache_len), on torch's current stream: the same token, K/V row and hidden
+    state as decode() at the same position, for any cache_len (unused, as in the
+    reference)."""
+    hw, w, packed = full
+    lib = _lib()
+    vp, i32, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+    lib.launch_ldg_decode_persistent.argtypes = [i32, vp] + [vp] * 19 + [i32, i32, i32, i32, f32, vp]
+    lib.launch_ldg_decode_persistent.restype = i32
+    ids = qw.synthetic_prompt(6, seed=21)
+    dec = qa.Decoder(weights=w, verbose=False)
+    ref = [dec.step(t) for t in ids]
+    ref_hidden = dec._hidden.clone()
+    dec2 = qa.Decoder(weights=w, verbose=False)
+    for t in ids[:-1]:
+        dec2.step(t)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ts = [t.data_ptr() for t in dec2._tensors()]
+    stream = torch.cuda.current_stream().cuda_stream
+    for cache_len in (len(ids), 0):
+        rc = lib.launch_ldg_decode_persistent(ids[-1], out.data_ptr(), *ts, 28, len(ids) - 1, cache_len, MAX_SEQ,
+                                              SCALE, stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert ext.last_error() == 0
+        assert int(out.item()) == ref[-1]
+        assert torch.equal(dec2._hidden, ref_hidden)
+        assert torch.equal(dec2._k_cache[:, :, len(ids) - 1], dec._k_cache[:, :, len(ids) - 1])
+
+
+def test_forced_timeout_recovery(ext, full, qa):
+    """The error path, forced from the host: with a 1 us budget per device-side wait the
+    kernel's bounded waits give up, every wave leaves, last_error() reports the timeout
+    (and resets the engine's workspace), Decoder raises, and after restoring the budget
+    the next run is bit-identical to one that never failed."""
+    hw, w, packed = full
+    ids = qw.synthetic_prompt(8, seed=31)
+    good = Run(w, packed, 28).forced(ext, ids, 0)
+    dec = qa.Decoder(weights=w, verbose=False)
+    ext.set_wait_deadline_us(1)
+    try:
+        with pytest.raises(RuntimeError, match="deadline"):
+            dec.generate_ids(ids, 4)
+        r = Run(w, packed, 28)
+        n = len(ids)
+        f = torch.tensor(ids, dtype=torch.int32, device="cuda")
+        ext.generate_ex(ids[0], n, f, w["embed_weight"], packed, w["final_norm_weight"], w["lm_head_weight"],
+                        w["cos_table"], w["sin_table"], r.kc, r.vc, r.hidden, r.norm_out, None, None, 28, 0, MAX_SEQ,
+                        SCALE)
+        torch.cuda.synchronize()
+        assert ext.last_error() == 4  # QWEN_ERR_TIMEOUT
+        assert ext.last_error() == 0  # reported once, then cleared
+    finally:
+        ext.set_wait_deadline_us(0)
+    again = Run(w, packed, 28).forced(ext, ids, 0)
+    assert again[0] == good[0]
+    assert torch.equal(again[1], good[1]) and torch.equal(again[2], good[2])
+    # the Decoder that raised works again (generate_ids resets it first)
+    assert dec.generate_ids(ids, 4) == qa.Decoder(weights=w, verbose=False).generate_ids(ids, 4)
 
 
 def test_full_model_golden_tokens_free_running(ext, full, qa):
@@ -279,6 +438,14 @@ def test_traced_kernel_matches_and_records(ext, full):
     assert bool((tr[..., 0] > 0).all()) and bool((tr[..., 3] > 0).all())
     assert bool((tr[..., 3] >= tr[..., 0]).all())
     assert ext.last_error() == 0
+    # a buffer too small for the launch's layers is refused before anything runs
+    ext.set_trace(buf[: 256 * fins * ev - 1], 3)
+    try:
+        with pytest.raises(RuntimeError):
+            Run(w, packed, L).forced(ext, ids, 0, logits=False, hidden=False)
+    finally:
+        ext.set_trace(None, 0)
+    assert ext.last_error() == 0
 
 
 def test_lm_head_argmax_1000_trials(ext, full):
@@ -333,6 +500,27 @@ def test_lm_head_exact_ties_lowest_index(ext, full):
             got = int(ext.lm_head_argmax(h, W).cpu()[0])
             assert got == lo_row, (lo_row, hi_row, got)
     assert ext.last_error() == 0
+
+
+def test_mlp_block_random_post_norm(ext, rn):
+    """Isolated MLP half-layer with a non-unit post-attention norm (layer 5 of the rn
+    model) and a residual of N(0, 1) values."""
+    hw, w, _ = rn
+    layer = hw.layers[5]
+    gate, up, down, norm = layer[8], layer[9], layer[10], layer[7]
+    assert float(np.abs(norm.astype(np.float32) - 1).max()) > 0.5
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    f32 = lambda a: torch.from_numpy(a).float()
+    worst = 0.0
+    for seed in range(5):
+        x = np.random.Generator(np.random.PCG64(700 + seed)).standard_normal(1024, dtype=np.float32).astype(np.float16)
+        y = ext.mlp_block(dev(x), dev(norm), dev(gate), dev(up), dev(down)).cpu()
+        ref = orc.mlp_block(f32(x), f32(norm), f32(gate), f32(up), f32(down))
+        err = float((y - ref).abs().max())
+        worst = max(worst, err)
+        assert err <= TOL_MLP, (seed, err)
+    assert ext.last_error() == 0
+    print(f"mlp block, random post-norm: worst max-abs {worst:.3e}")
 
 
 def test_mlp_block(ext, full):

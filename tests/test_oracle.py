@@ -138,6 +138,72 @@ def test_swiglu_and_mlp_block_brute_force():
     assert torch.allclose(orc.mlp_block(x, w, wg, wu, wd), x + orc.swiglu_mlp(orc.rms_norm(x, w), wg, wu, wd))
 
 
+def test_mlp_block_brute_force_nonunit_norm_and_residual():
+    """The isolated-MLP oracle against explicit float64 loops: RMSNorm written out
+    (sum of squares, eps inside the root, per-element gain), SiLU as g / (1 + e^-g),
+    the down projection and the residual add. A dropped gain, a missing residual or
+    eps outside the root fails this."""
+    g = torch.Generator().manual_seed(13)
+    h, i = 16, 24
+    x = torch.randn(h, generator=g, dtype=torch.float64) * 3
+    wn = 1.0 + 0.5 * torch.randn(h, generator=g, dtype=torch.float64)
+    wg = torch.randn(i, h, generator=g, dtype=torch.float64) * 0.3
+    wu = torch.randn(i, h, generator=g, dtype=torch.float64) * 0.3
+    wd = torch.randn(h, i, generator=g, dtype=torch.float64) * 0.3
+    xs = [float(v) for v in x]
+    rms = math.sqrt(sum(v * v for v in xs) / h + orc.EPS)
+    hn = [xs[c] / rms * float(wn[c]) for c in range(h)]
+    inter = []
+    for j in range(i):
+        gj = sum(float(wg[j, c]) * hn[c] for c in range(h))
+        uj = sum(float(wu[j, c]) * hn[c] for c in range(h))
+        inter.append(gj / (1.0 + math.exp(-gj)) * uj)
+    ref = [xs[r] + sum(float(wd[r, j]) * inter[j] for j in range(i)) for r in range(h)]
+    out = orc.mlp_block(x, wn, wg, wu, wd)
+    assert torch.allclose(out, torch.tensor(ref, dtype=torch.float64), rtol=1e-12, atol=1e-12)
+    # the gain is really applied: unit gain gives a different answer
+    assert float((out - orc.mlp_block(x, torch.ones(h, dtype=torch.float64), wg, wu, wd)).abs().max()) > 1e-3
+
+
+def test_top2_gap_closed_forms():
+    """The near-tie exemption's gap: an exact tie is 0, otherwise max minus the
+    runner-up (not minus the minimum, not the top-2 of the absolute values)."""
+    assert orc.top2_gap(torch.tensor([1.0, 3.0, 3.0, 2.0])) == 0.0
+    assert orc.top2_gap(torch.tensor([5.0, 1.0, 2.0])) == 3.0
+    assert orc.top2_gap(torch.tensor([-1.0, -4.0])) == 3.0
+    assert orc.top2_gap(torch.tensor([-7.0, 0.5, -0.25, 0.0])) == 0.5
+    x = torch.randn(100000, generator=torch.Generator().manual_seed(6))
+    x[4242] = float(x.max()) + 0.25
+    ranked = sorted(x.tolist(), reverse=True)
+    assert abs(orc.top2_gap(x) - (ranked[0] - ranked[1])) < 1e-6
+    assert abs(orc.top2_gap(x) - 0.25) < 1e-6
+
+
+def test_forward_matches_steps_and_is_chunkable():
+    """The batched causal forward (prefill) against n single steps of the oracle on a
+    model with non-unit norms and an untied lm_head: same K/V cache, hidden states
+    and logits; and a forward split in two chunks equals one forward over all ids."""
+    hw = qw.host_weights(seed=7, std=0.2, shape=TINY, norms="random", untied=True)
+    ids = qw.synthetic_prompt(30, seed=5, vocab=TINY.vocab)
+    a, b, c = orc.Oracle(hw), orc.Oracle(hw), orc.Oracle(hw)
+    steps = [a.step(t, p) for p, t in enumerate(ids)]
+    whole = b.forward(ids, logits_at=range(len(ids)))
+    c.forward(ids[:11])
+    tail = c.forward(ids[11:], start=11, logits_at=range(11, len(ids)))
+    for p, st in enumerate(steps):
+        # fp32 sums in another order: relative agreement of ~1e-6 on values of O(10)
+        assert torch.allclose(whole["hidden"][p], st["hidden"], rtol=1e-5, atol=1e-4), p
+        assert torch.allclose(whole["logits"][p], st["logits"], rtol=1e-5, atol=1e-4), p
+        assert whole["tokens"][p] == st["token"]
+    assert torch.allclose(a.k_cache, b.k_cache, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(a.v_cache, b.v_cache, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(b.k_cache, c.k_cache, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(tail["logits"], whole["logits"][11:], rtol=1e-5, atol=1e-4)
+    # the untied lm_head is the one used: the tied embedding gives other logits
+    tied = orc.lm_head_logits(b.embed, whole["norm_out"][-1])
+    assert float((tied - whole["logits"][-1]).abs().max()) > 1e-2
+
+
 def test_argmax_planted_ties_and_nan():
     g = torch.Generator().manual_seed(4)
     W = torch.randn(5000, 64, generator=g)
@@ -152,6 +218,7 @@ def test_argmax_planted_ties_and_nan():
 
 def _hf_model(hw, shape):
     transformers = pytest.importorskip("transformers")
+    tied = hw.lm_head is None
     cfg = transformers.Qwen3Config(
         vocab_size=shape.vocab,
         hidden_size=shape.hidden,
@@ -163,7 +230,7 @@ def _hf_model(hw, shape):
         max_position_embeddings=shape.max_seq,
         rms_norm_eps=shape.eps,
         rope_parameters={"rope_type": "default", "rope_theta": shape.rope_theta},
-        tie_word_embeddings=True,
+        tie_word_embeddings=tied,
         attention_bias=False,
     )
     model = transformers.Qwen3ForCausalLM(cfg).float().eval()
@@ -175,23 +242,22 @@ def _hf_model(hw, shape):
     for li, layer in enumerate(hw.layers):
         for n, t in zip(names, layer):
             sd[f"model.layers.{li}.{n}.weight"] = f32(t)
-    sd["lm_head.weight"] = sd["model.embed_tokens.weight"]
+    sd["lm_head.weight"] = sd["model.embed_tokens.weight"] if tied else f32(hw.lm_head)
     missing, unexpected = model.load_state_dict(sd, strict=False)
     assert not unexpected and all("lm_head" in m for m in missing)
+    if not tied:
+        assert not missing
+        assert torch.equal(model.lm_head.weight, f32(hw.lm_head))
     return model
 
 
-@pytest.mark.parametrize("std", [0.02, 0.2])
-def test_oracle_matches_huggingface_qwen3(std):
-    """End-to-end: the oracle's step-by-step decode equals HF Qwen3's causal
-    forward over the same ids (fp32 both, fp32 RoPE tables), and greedy tokens
-    agree. Non-unit norm weights exercise every norm's weight multiply."""
-    hw = qw.host_weights(seed=7, std=std, shape=TINY)
-    rng = np.random.default_rng(11)
-    for layer in hw.layers:
-        for f in qw.NORM_FIELDS:
-            layer[f] = (1.0 + 0.5 * rng.standard_normal(layer[f].shape)).astype(np.float16)
-    hw.final_norm = (1.0 + 0.5 * rng.standard_normal(hw.final_norm.shape)).astype(np.float16)
+@pytest.mark.parametrize("std,untied", [(0.02, False), (0.2, False), (0.2, True)])
+def test_oracle_matches_huggingface_qwen3(std, untied):
+    """End-to-end: the oracle's step-by-step decode and its batched forward both equal
+    HF Qwen3's causal forward over the same ids (fp32 both, fp32 RoPE tables), and
+    greedy tokens agree. Non-unit norm weights (distinct per layer and field) exercise
+    every norm's weight multiply; the untied case, HF's separate lm_head."""
+    hw = qw.host_weights(seed=7, std=std, shape=TINY, norms="random", untied=untied)
     prompt = qw.synthetic_prompt(6, seed=5, vocab=TINY.vocab)
     oracle = orc.Oracle(hw, rope="fp32")
     run = oracle.greedy(prompt, n_new=10)
@@ -203,6 +269,8 @@ def test_oracle_matches_huggingface_qwen3(std):
         ref = logits[len(prompt) - 1 + i]
         assert torch.allclose(st["logits"], ref, atol=2e-5, rtol=1e-5), (i, float((st["logits"] - ref).abs().max()))
         assert st["token"] == int(torch.argmax(ref))
+    fwd = orc.Oracle(hw, rope="fp32").forward(ids, logits_at=range(len(ids)))
+    assert torch.allclose(fwd["logits"], logits, atol=2e-5, rtol=1e-5), float((fwd["logits"] - logits).abs().max())
 
 
 def test_fp16_rope_tables_stay_close_to_fp32():
