@@ -135,6 +135,26 @@ int qwen_generate_until(
     int* output_log, int* out_count, int num_layers, int start_position,
     int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* launch_ldg_generate_nosync without any allocation, for callers that cannot
+ * allocate device memory (code under stream capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Same
+ * arguments, limits and results as launch_ldg_generate_nosync; its exchange
+ * workspace is a fixed 1,564,928-byte array in the library's device memory
+ * (one per GPU, held until the process ends) instead of the allocated one, and
+ * memory is cleared with a kernel, never hipMemset. Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, two threads)
+ * race and must be serialized by the caller. Errors are reported by
+ * qwen_last_error(). */
+int qwen_generate_nosync_noalloc(
+    int first_token_id, int num_steps, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_activations,
+    void* g_residual, void* g_q, void* g_k, void* g_v, void* g_attn_out,
+    void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+    void* block_max_idxs, int* output_log, int num_layers, int start_position,
+    int max_seq_len, float attn_scale, hipStream_t stream);
+
 /* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */

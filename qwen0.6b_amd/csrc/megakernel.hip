@@ -123,6 +123,18 @@ __global__ void __launch_bounds__(BLOCK, 1) qwen_placement_probe(u32* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
+// zeroes n 8-byte words (a kernel, not hipMemsetAsync: callers may capture the stream)
+__global__ void qwen_zero_words(u64* p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// Exchange workspace of qwen_generate_nosync_noalloc: the same layout as the workspace the
+// other entry points allocate (slots, status line, lm_head pool counters), as module memory,
+// one copy per device. Host code never uses this name as an address: it uses the pointer
+// hipGetSymbolAddress returns for the current device (DeviceState::fixed).
+static_assert(WORKSPACE_BYTES % 256 == 0, "whole 256-byte lines");
+static __device__ __align__(256) unsigned char scratch[WORKSPACE_BYTES];
+
 // ------------------------------------------------------------------------------------
 // host side
 
@@ -131,13 +143,19 @@ namespace {
 constexpr int MAX_DEVICES = 16;
 constexpr u64 DEFAULT_WAIT_US = 500000;
 
+// one exchange workspace (WORKSPACE_BYTES) and the token epoch its tags continue from
+struct Workspace {
+  u64* ws = nullptr;
+  u32* status = nullptr;
+  u32 epoch = 1;
+};
+
 struct DeviceState {
   bool init = false;
   int err = QWEN_OK;
-  u64* ws = nullptr;
-  u32* status = nullptr;
+  Workspace heap;                 // hipMalloc'd on first use by the allocating entry points
+  Workspace fixed;                // the `scratch` array of this device (no allocation)
   LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
-  u32 epoch = 1;
   u64 clk_khz = 100000;
   u64 deadline = 0;
   u64* trace = nullptr;
@@ -155,23 +173,29 @@ void teardown() {
   std::lock_guard<std::mutex> lock(g_mu);
   for (int d = 0; d < MAX_DEVICES; ++d) {
     DeviceState& st = g_dev[d];
-    if (!st.ws && !st.tab) continue;
+    if (!st.heap.ws && !st.tab) continue;
     if (hipSetDevice(d) != hipSuccess) continue;
     (void)hipDeviceSynchronize();
-    if (st.ws) (void)hipFree(st.ws);
+    if (st.heap.ws) (void)hipFree(st.heap.ws);
     if (st.tab) (void)hipFree(st.tab);
     st = DeviceState();
   }
 }
 
+int zero_words(void* p, long bytes, hipStream_t s) {
+  hipLaunchKernelGGL(qwen_zero_words, dim3(NWG), dim3(256), 0, s, (u64*)p, bytes / 8);
+  return hipGetLastError() == hipSuccess ? QWEN_OK : QWEN_ERR_LAUNCH;
+}
+
 // Every workgroup w of a 256 x 512 launch must run on XCD w % 8: the work partition and the
-// XCD-local exchange stores rely on it. Checked once per device with a probe launch.
-int check_placement(u32* scratch, hipStream_t s) {
-  void* args[] = {&scratch};
+// XCD-local exchange stores rely on it. Checked once per device with a probe launch that
+// writes into `buf` (NWG words).
+int check_placement(u32* buf, hipStream_t s) {
+  void* args[] = {&buf};
   if (hipLaunchCooperativeKernel((const void*)qwen_placement_probe, dim3(NWG), dim3(BLOCK), args, 0, s) != hipSuccess)
     return QWEN_ERR_LAUNCH;
   u32 xcc[NWG];
-  if (hipMemcpy(xcc, scratch, sizeof(xcc), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
+  if (hipMemcpy(xcc, buf, sizeof(xcc), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
   for (int w = 0; w < NWG; ++w)
     if ((int)(xcc[w] & 15) != xcd_of(w)) {
       fprintf(stderr, "qwen_megakernel: workgroup %d runs on XCC %u, the work partition needs XCC %d\n", w,
@@ -181,18 +205,19 @@ int check_placement(u32* scratch, hipStream_t s) {
   return QWEN_OK;
 }
 
+// Device checks and the fixed workspace, once per device; allocates nothing. (Caller holds g_mu.)
 int device_state(DeviceState** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return QWEN_ERR_DEVICE;
   DeviceState& st = g_dev[dev];
   if (!st.init) {
+    st.init = true;
+    st.err = QWEN_ERR_DEVICE;
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return QWEN_ERR_DEVICE;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return st.err;
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0 || prop.multiProcessorCount != NWG || !prop.cooperativeLaunch) {
       fprintf(stderr, "qwen_megakernel: needs a 256-CU gfx950 device with cooperative launch (got %s, %d CUs)\n",
               prop.gcnArchName, prop.multiProcessorCount);
-      st.err = QWEN_ERR_DEVICE;
-      st.init = true;
       return st.err;
     }
     int occ = 0;
@@ -200,57 +225,74 @@ int device_state(DeviceState** out) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)fast::qwen_decode_kernel, BLOCK, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_t, (const void*)traced::qwen_decode_kernel, BLOCK, 0) !=
             hipSuccess ||
-        occ_t < 1 ||
-        occ < 1) {
-      st.err = QWEN_ERR_DEVICE;
-      st.init = true;
+        occ_t < 1 || occ < 1)
       return st.err;
-    }
     int clk_khz = 0;
     if (hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || clk_khz <= 0)
       clk_khz = 100000;
     st.clk_khz = (u64)clk_khz;
     st.deadline = st.clk_khz * DEFAULT_WAIT_US / 1000;  // 0.5 s per single wait
-    void* p = nullptr;
-    if (hipMalloc(&p, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-    std::call_once(g_teardown_once, [] { std::atexit(teardown); });
-    st.ws = (u64*)p;
-    const int pc = check_placement((u32*)p, nullptr);
-    if (pc != QWEN_OK) {
-      st.err = pc;
-      st.init = true;
+    // this device's copy of `scratch`: its address, never the host-side name
+    void* fixed = nullptr;
+    if (hipGetSymbolAddress(&fixed, HIP_SYMBOL(scratch)) != hipSuccess || fixed == nullptr) {
+      st.err = QWEN_ERR_LAUNCH;
       return st.err;
     }
-    if (hipMemset(p, 0, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-    st.status = (u32*)((char*)p + TOTAL_SLOTS * 8);
-    st.init = true;
+    st.err = check_placement((u32*)fixed, nullptr);
+    if (st.err != QWEN_OK) return st.err;
+    if (zero_words(fixed, WORKSPACE_BYTES, nullptr) != QWEN_OK || hipDeviceSynchronize() != hipSuccess) {
+      st.err = QWEN_ERR_LAUNCH;
+      return st.err;
+    }
+    st.fixed.ws = (u64*)fixed;
+    st.fixed.status = (u32*)((char*)fixed + TOTAL_SLOTS * 8);
+    st.err = QWEN_OK;
   }
   if (st.err != QWEN_OK) return st.err;
   *out = &st;
   return QWEN_OK;
 }
 
-int launch(KParams& P, hipStream_t stream) {
+// The allocating entry points' workspace, on first use. (Caller holds g_mu.)
+int heap_workspace(DeviceState* st) {
+  if (st->heap.ws) return QWEN_OK;
+  void* p = nullptr;
+  if (hipMalloc(&p, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+  std::call_once(g_teardown_once, [] { std::atexit(teardown); });
+  if (hipMemset(p, 0, WORKSPACE_BYTES) != hipSuccess) {
+    (void)hipFree(p);
+    return QWEN_ERR_LAUNCH;
+  }
+  st->heap.ws = (u64*)p;
+  st->heap.status = (u32*)((char*)p + TOTAL_SLOTS * 8);
+  return QWEN_OK;
+}
+
+// launches the decode kernel on the heap workspace, or (fixed = true) on the device's
+// `scratch` array, in which case nothing is allocated
+int launch(KParams& P, hipStream_t stream, bool fixed = false) {
   std::lock_guard<std::mutex> lock(g_mu);
   DeviceState* st = nullptr;
   int rc = device_state(&st);
   if (rc != QWEN_OK) return rc;
+  if (!fixed && (rc = heap_workspace(st)) != QWEN_OK) return rc;
+  Workspace& w = fixed ? st->fixed : st->heap;
   // a trace buffer must hold every stage of every workgroup of this launch's layers
   if (st->trace && (long long)NWG * trace_stages(P.num_layers) * TRACE_EVENTS > st->trace_elems) return QWEN_ERR_ARG;
-  P.ws = st->ws;
-  P.status = st->status;
+  P.ws = w.ws;
+  P.status = w.status;
   P.deadline = st->deadline;
   P.trace = st->trace;
   P.trace_token = st->trace_token;
-  P.epoch0 = st->epoch;
+  P.epoch0 = w.epoch;
   // epochs are 24-bit in the tag; wrap back to 1 (never 0: a zeroed slot is never "ready")
-  u64 next = (u64)st->epoch + (u64)P.num_steps + 1;
+  u64 next = (u64)w.epoch + (u64)P.num_steps + 1;
   if (next >= (1u << 24)) {
-    if (hipMemsetAsync(st->ws, 0, TOTAL_SLOTS * 8, stream) != hipSuccess) return QWEN_ERR_LAUNCH;
+    if (zero_words(w.ws, TOTAL_SLOTS * 8, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
     P.epoch0 = 1;
     next = 1 + (u64)P.num_steps + 1;
   }
-  st->epoch = (u32)next;
+  w.epoch = (u32)next;
   void* args[] = {&P};
   const void* kernel = P.trace ? (const void*)traced::qwen_decode_kernel : (const void*)fast::qwen_decode_kernel;
   if (hipLaunchCooperativeKernel(kernel, dim3(NWG), dim3(BLOCK), args, 0, stream) != hipSuccess)
@@ -379,6 +421,28 @@ extern "C" int launch_ldg_generate_nosync(int first_token_id, int num_steps, con
                           output_log, nullptr, nullptr, num_layers, start_position, max_seq_len, attn_scale, stream);
 }
 
+// launch_ldg_generate_nosync on the device's fixed `scratch` workspace: no allocation in this
+// call or in its first-use set-up on a device. The workspace need does not depend on the
+// arguments; their limits are those of launch_ldg_generate_nosync (QWEN_ERR_ARG beyond them).
+extern "C" int qwen_generate_nosync_noalloc(int first_token_id, int num_steps, const void* embed_weight,
+                                            const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+                                            const void* lm_head_weight, const void* cos_table,
+                                            const void* sin_table, void* k_cache, void* v_cache,
+                                            void* hidden_buffer, void*, void*, void*, void*, void*, void*, void*,
+                                            void* g_normalized, void*, void*, int* output_log, int num_layers,
+                                            int start_position, int max_seq_len, float attn_scale,
+                                            hipStream_t stream) {
+  KParams P;
+  int rc = fill_decode(P, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                       k_cache, v_cache, hidden_buffer, g_normalized, num_layers, start_position, num_steps,
+                       max_seq_len, attn_scale);
+  if (rc != QWEN_OK) return rc;
+  if (!output_log || first_token_id < 0 || first_token_id >= VOCAB) return QWEN_ERR_ARG;
+  P.first_token = first_token_id;
+  P.out_tokens = output_log;
+  return launch(P, stream, /*fixed=*/true);
+}
+
 extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token, float* logits_out,
                                    hipStream_t stream) {
   if (!hidden_f16 || !weight || !out_token || !aligned16(hidden_f16) || !aligned16(weight)) return QWEN_ERR_ARG;
@@ -417,6 +481,7 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
     int rc = device_state(&st);
     if (rc != QWEN_OK) return rc;
     if (!st->tab && hipMalloc(&st->tab, sizeof(LDGLayerWeight)) != hipSuccess) return QWEN_ERR_LAUNCH;
+    std::call_once(g_teardown_once, [] { std::atexit(teardown); });
     tab = st->tab;
   }
   if (hipMemcpyAsync(tab, &h, sizeof(h), hipMemcpyHostToDevice, stream) != hipSuccess) return QWEN_ERR_LAUNCH;
@@ -434,6 +499,24 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
   return launch(P, stream);
 }
 
+namespace {
+
+// status word of one workspace: 0, or the error it reports (the workspace is then cleared
+// and its epochs restart)
+int take_status(Workspace& w) {
+  if (!w.ws) return QWEN_OK;
+  u32 s = 0;
+  if (hipMemcpy(&s, w.status, sizeof(s), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
+  if (s == 0) return QWEN_OK;
+  // a failed launch leaves slots in an unknown state: start clean
+  if (zero_words(w.ws, WORKSPACE_BYTES, nullptr) != QWEN_OK || hipDeviceSynchronize() != hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  w.epoch = 1;
+  return (s & ST_BAD_TOKEN) ? QWEN_ERR_BAD_TOKEN : QWEN_ERR_TIMEOUT;
+}
+
+}  // namespace
+
 extern "C" int qwen_last_error(void) {
   std::lock_guard<std::mutex> lock(g_mu);
   int dev = 0;
@@ -442,14 +525,9 @@ extern "C" int qwen_last_error(void) {
   if (!st.init) return QWEN_OK;
   if (st.err != QWEN_OK) return st.err;
   if (hipDeviceSynchronize() != hipSuccess) return QWEN_ERR_LAUNCH;
-  u32 s = 0;
-  if (hipMemcpy(&s, st.status, sizeof(s), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
-  if (s == 0) return QWEN_OK;
-  // a failed launch leaves slots in an unknown state: start clean
-  if (hipMemset(st.ws, 0, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-  st.epoch = 1;
-  if (s & ST_BAD_TOKEN) return QWEN_ERR_BAD_TOKEN;
-  return QWEN_ERR_TIMEOUT;
+  const int a = take_status(st.heap);
+  const int b = take_status(st.fixed);
+  return a != QWEN_OK ? a : b;
 }
 
 extern "C" int qwen_set_wait_deadline_us(long long us) {
