@@ -206,6 +206,89 @@ def run_mlp(args):
                     args.steps, args.warmup)
 
 
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def prefill_flops(n, start=0, layers=28):
+    """Algorithmic flops of a batched prefill of n positions after `start` cached ones:
+    the four projections (2 flops per weight per position) and causal attention (q.k and
+    p.v over the keys each position sees, 16 q heads x 128 dims)."""
+    gemm = 2 * n * LAYER_MATRIX_BYTES // 2  # weights per layer = bytes / 2
+    keys = sum(start + i + 1 for i in range(n))
+    attn = 2 * 2 * 16 * 128 * keys
+    return layers * (gemm + attn)
+
+
+def run_prefill(args):
+    """Batched prefill of a 1920-id prompt (the context the headline decode starts from), one
+    launch of the MFMA prefill kernel per step; counterpart of the reference's prefill timing
+    (Model/benchmark.py:112-125), which runs one decode step per id."""
+    import torch
+
+    import qwen_weights as qw
+    import Qwen06B_architecture as qa
+
+    w = qw.device_weights(qw.host_weights(seed=0, std=0.02), "cuda")
+    dec = qa.Decoder(weights=w, verbose=False)
+    prompt = qw.synthetic_prompt(PREFILL, seed=1)
+    ts = []
+    for rep in range(args.warmup + args.steps):
+        dec.reset()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec._prefill_kv(prompt)
+        e1.record()
+        torch.cuda.synchronize()
+        if rep >= args.warmup:
+            ts.append(e0.elapsed_time(e1))
+    qa._check_device_errors()
+    ms = _median(ts)
+    flops = prefill_flops(PREFILL)
+    tflops = flops / (ms / 1e3) / 1e12
+    return {
+        "metric": f"batched prefill tokens/sec ({PREFILL}-id prompt, 28 layers, one launch)",
+        "value": round(PREFILL / ms * 1e3, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic: seeded N(0,0.02) fp16 weights (norms 1.0)",
+        "config": {"workload": "prefill", "prompt": PREFILL, "layers": 28},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "pf::qwen_prefill_kernel", "flops_per_launch": flops, "kernel_ms": round(ms, 4)},
+        "cpu_baseline": None,
+    }
+
+
+def run_generate_e2e(args):
+    """Decoder.generate_ids of a 1000-id prompt with 1000 new tokens, prefill included in
+    the time, as the reference's benchmark times Decoder.generate (Model/benchmark.py:87-109,
+    tokens/s = new tokens / elapsed)."""
+    import torch
+
+    import qwen_weights as qw
+    import Qwen06B_architecture as qa
+
+    w = qw.device_weights(qw.host_weights(seed=0, std=0.02), "cuda")
+    dec = qa.Decoder(weights=w, verbose=False)
+    n_prompt, n_new = 1000, 1000
+    prompt = qw.synthetic_prompt(n_prompt, seed=1)
+    ts = []
+    for rep in range(args.warmup + args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = dec.generate_ids(prompt, n_new)
+        dt = time.perf_counter() - t0
+        if rep >= args.warmup:
+            ts.append(dt * 1e3)
+    assert len(out) == n_new
+    ms = _median(ts)
+    return aux_line("Decoder.generate tokens/sec, 1000-id prompt + 1000 new tokens, prefill included",
+                    round(n_new / ms * 1e3, 2), "tokens/s", True, "generate",
+                    {"prompt": n_prompt, "new_tokens": n_new, "positions": f"0..{n_prompt + n_new - 2}"},
+                    "fast::qwen_decode_kernel + pf::qwen_prefill_kernel",
+                    algorithmic_bytes(n_prompt - 1, n_new), ms, args.steps, args.warmup)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,9 +301,11 @@ def main():
     ap.add_argument("--trace", default=None,
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
                          "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, events], 100 MHz ticks)")
-    ap.add_argument("--workload", choices=["c4", "c3", "c0", "c1", "c2"], default="c4",
+    ap.add_argument("--workload", choices=["c4", "c3", "c0", "c1", "c2", "prefill", "generate"], default="c4",
                     help="c4 (default): the headline decode at context 1921..2048; c3: 128-id prompt + "
-                         "generate_nosync 512; c0: 16 + 32; c1: isolated lm_head + argmax; c2: isolated MLP block")
+                         "generate_nosync 512; c0: 16 + 32; c1: isolated lm_head + argmax; c2: isolated MLP block; "
+                         "prefill: batched prefill of 1920 ids; generate: Decoder.generate_ids 1000 + 1000 "
+                         "with its prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine runs one sequence on one MI355X; --gpus {args.gpus} "
@@ -229,7 +314,8 @@ def main():
 
     if args.workload != "c4":
         runs = {"c3": lambda: run_generate(args, 128, 512, "c3"), "c0": lambda: run_generate(args, 16, 32, "c0"),
-                "c1": lambda: run_lm_head(args), "c2": lambda: run_mlp(args)}
+                "c1": lambda: run_lm_head(args), "c2": lambda: run_mlp(args),
+                "prefill": lambda: run_prefill(args), "generate": lambda: run_generate_e2e(args)}
         print(json.dumps(runs[args.workload]()), flush=True)
         return
 

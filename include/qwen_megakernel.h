@@ -155,6 +155,22 @@ int qwen_generate_nosync_noalloc(
     void* block_max_idxs, int* output_log, int num_layers, int start_position,
     int max_seq_len, float attn_scale, hipStream_t stream);
 
+/* Batched prefill (no counterpart in the reference, which prefills with one
+ * decode step per id, Model/Qwen06B_architecture.py:346-347): the n ids
+ * (device int32[n]) at positions start_position .. start_position + n - 1 run
+ * through all num_layers layers in one launch, as matrix products on MFMA;
+ * writes the K/V cache of every one of those positions and, to hidden_buffer,
+ * the last position's final-layer residual. No lm_head: the greedy token after
+ * a prompt comes from a decode step of its last id. Ids outside [0, 151936)
+ * are reported by qwen_last_error() (QWEN_ERR_BAD_TOKEN). Allocates a 36 MB
+ * activation workspace per device on first use. */
+int qwen_prefill(
+    const int* ids, int n, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* cos_table,
+    const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+    int num_layers, int start_position, int max_seq_len, float attn_scale,
+    hipStream_t stream);
+
 /* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */

@@ -14,8 +14,8 @@ Differences from the reference, all additive:
   (safetensors) instead of downloading; ``qwen_weights.synthetic_weights``
   builds seeded random weights in the same dictionary layout;
 * ``Decoder.prefill`` / ``generate_ids`` run a prompt and greedy generation on
-  token ids (no tokenizer needed); the prompt is prefilled in one launch with
-  teacher forcing instead of one launch and host sync per token;
+  token ids (no tokenizer needed); the prompt is prefilled in one launch of the
+  batched (MFMA) prefill kernel instead of one launch and host sync per token;
 * positions beyond ``MAX_SEQ_LEN`` raise instead of silently skipping
   attention (Tools/megakernel/megakernel.cu:330-333);
 * device-side errors are checked after every synchronising call.
@@ -311,14 +311,33 @@ class Decoder:
         self._position += num_steps
         return out
 
-    def prefill(self, ids) -> int:
-        """Run every id in ``ids`` through the model at consecutive positions in one
-        launch (teacher forced); returns the greedy token after the last id."""
+    def _prefill_kv(self, ids) -> None:
+        """Write the K/V cache of ``ids`` at positions ``position ..`` in one batched launch
+        (MFMA prefill kernel) and advance the position; no greedy token."""
+        if not ids:
+            return
+        if self._position + len(ids) > MAX_SEQ_LEN:
+            raise RuntimeError(f"prefill of {len(ids)} ids at position {self._position} exceeds {MAX_SEQ_LEN}")
+        t = torch.tensor(ids, dtype=torch.int32, device=DEVICE)
+        qwen_megakernel_C.prefill(t, self._embed_weight, self._layer_weights_packed, self._cos_table,
+                                  self._sin_table, self._k_cache, self._v_cache, self._hidden, self._num_layers,
+                                  self._position, MAX_SEQ_LEN, self._attn_scale)
+        self._position += len(ids)
+
+    def prefill(self, ids, batched: bool = True) -> int:
+        """Run every id in ``ids`` through the model at consecutive positions; returns the
+        greedy token after the last id (the reference prefills with one ``step`` per id,
+        lines 346-347). ``batched``: all but the last id in one launch of the batched
+        (MFMA) prefill kernel, then one decode step of the last id; otherwise every id
+        teacher forced through the decode kernel in one launch."""
         ids = [int(t) for t in ids]
         if not ids:
             raise ValueError("prefill needs at least one id")
         if self._position + len(ids) > MAX_SEQ_LEN:
             raise RuntimeError(f"prefill of {len(ids)} ids at position {self._position} exceeds {MAX_SEQ_LEN}")
+        if batched:
+            self._prefill_kv(ids[:-1])
+            ids = ids[-1:]
         forced = torch.tensor(ids, dtype=torch.int32, device=DEVICE)
         out = qwen_megakernel_C.generate_ex(
             ids[0], len(ids), forced, self._embed_weight, self._layer_weights_packed, self._final_norm_weight,
@@ -351,8 +370,7 @@ class Decoder:
         ``eos_token_id`` the device stops after that id (which ends the list)."""
         self.reset()
         ids = [int(t) for t in ids]
-        if len(ids) > 1:
-            self.prefill(ids[:-1])
+        self._prefill_kv(ids[:-1])
         if eos_token_id is not None:
             return self.generate_until(ids[-1], max_tokens, eos_token_id)
         out = self.generate_nosync(ids[-1], max_tokens).cpu().tolist()

@@ -118,6 +118,9 @@ constexpr bool kTrace = true;
 #include "decode_body.inc"
 }  // namespace traced
 
+// the batched prefill kernel (namespace pf)
+#include "prefill_body.inc"
+
 // one workgroup per CU, as the decode kernel: each records the XCC it runs on
 __global__ void __launch_bounds__(BLOCK, 1) qwen_placement_probe(u32* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
@@ -156,6 +159,7 @@ struct DeviceState {
   Workspace heap;                 // hipMalloc'd on first use by the allocating entry points
   Workspace fixed;                // the `scratch` array of this device (no allocation)
   LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
+  char* pf = nullptr;             // prefill activations (PF_BYTES), on first use
   u64 clk_khz = 100000;
   u64 deadline = 0;
   u64* trace = nullptr;
@@ -173,11 +177,12 @@ void teardown() {
   std::lock_guard<std::mutex> lock(g_mu);
   for (int d = 0; d < MAX_DEVICES; ++d) {
     DeviceState& st = g_dev[d];
-    if (!st.heap.ws && !st.tab) continue;
+    if (!st.heap.ws && !st.tab && !st.pf) continue;
     if (hipSetDevice(d) != hipSuccess) continue;
     (void)hipDeviceSynchronize();
     if (st.heap.ws) (void)hipFree(st.heap.ws);
     if (st.tab) (void)hipFree(st.tab);
+    if (st.pf) (void)hipFree(st.pf);
     st = DeviceState();
   }
 }
@@ -299,6 +304,15 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
     return QWEN_ERR_LAUNCH;
   return QWEN_OK;
 }
+
+// prefill activations for up to MAX_SEQ_LIMIT positions: residual X fp32 [n, 1024], q and the
+// attention output fp16 [n, 2048] each, SiLU * up fp16 [n, 3072], then the barrier counter
+constexpr long PF_X = 0;
+constexpr long PF_Q = PF_X + (long)MAX_SEQ_LIMIT * HIDDEN * 4;
+constexpr long PF_AO = PF_Q + (long)MAX_SEQ_LIMIT * QSZ * 2;
+constexpr long PF_IM = PF_AO + (long)MAX_SEQ_LIMIT * QSZ * 2;
+constexpr long PF_BAR = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
+constexpr long PF_BYTES = PF_BAR + 256;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -441,6 +455,62 @@ extern "C" int qwen_generate_nosync_noalloc(int first_token_id, int num_steps, c
   P.first_token = first_token_id;
   P.out_tokens = output_log;
   return launch(P, stream, /*fixed=*/true);
+}
+
+extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, const LDGLayerWeight* layer_weights,
+                            const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                            void* hidden_buffer, int num_layers, int start_position, int max_seq_len,
+                            float attn_scale, hipStream_t stream) {
+  if (!ids || !embed_weight || !layer_weights || !cos_table || !sin_table || !k_cache || !v_cache || !hidden_buffer)
+    return QWEN_ERR_ARG;
+  if (!aligned16(embed_weight) || !aligned16(layer_weights) || !aligned16(cos_table) || !aligned16(sin_table) ||
+      !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(hidden_buffer))
+    return QWEN_ERR_ARG;
+  if (n < 1 || num_layers < 1 || num_layers > MAX_LAYERS || start_position < 0 || max_seq_len < 4 ||
+      (max_seq_len & 3) != 0 || max_seq_len > MAX_SEQ_LIMIT || (long)start_position + n > (long)max_seq_len)
+    return QWEN_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceState* st = nullptr;
+  int rc = device_state(&st);
+  if (rc != QWEN_OK) return rc;
+  if ((rc = heap_workspace(st)) != QWEN_OK) return rc;
+  if (!st->pf) {
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)pf::qwen_prefill_kernel, pf::NT, 0) !=
+            hipSuccess || occ < 1)
+      return QWEN_ERR_DEVICE;
+    void* p = nullptr;
+    if (hipMalloc(&p, PF_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+    st->pf = (char*)p;
+  }
+  pf::PParams P;
+  memset(&P, 0, sizeof(P));
+  P.ids = ids;
+  P.embed = (const _Float16*)embed_weight;
+  P.layers = layer_weights;
+  P.cos_t = (const _Float16*)cos_table;
+  P.sin_t = (const _Float16*)sin_table;
+  P.kc = (_Float16*)k_cache;
+  P.vc = (_Float16*)v_cache;
+  P.hidden_out = (_Float16*)hidden_buffer;
+  P.X = (float*)(st->pf + PF_X);
+  P.Q = (_Float16*)(st->pf + PF_Q);
+  P.AO = (_Float16*)(st->pf + PF_AO);
+  P.IM = (_Float16*)(st->pf + PF_IM);
+  P.bar = (u32*)(st->pf + PF_BAR);
+  P.status = st->heap.status;
+  P.deadline = st->deadline;
+  P.n = n;
+  P.start = start_position;
+  P.num_layers = num_layers;
+  P.max_seq = max_seq_len;
+  P.attn_scale = attn_scale;
+  if (zero_words(P.bar, 256, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
+  void* args[] = {&P};
+  if (hipLaunchCooperativeKernel((const void*)pf::qwen_prefill_kernel, dim3(NWG), dim3(pf::NT), args, 0, stream) !=
+      hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  return QWEN_OK;
 }
 
 extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token, float* logits_out,

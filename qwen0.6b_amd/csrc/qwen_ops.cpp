@@ -188,6 +188,33 @@ std::tuple<torch::Tensor, torch::Tensor> generate_until(int first_token_id, int 
   return {out, count};
 }
 
+// batched prefill of `ids` (int32 device tensor) at start_position ..; writes K/V and hidden
+void prefill(torch::Tensor ids, torch::Tensor embed_weight, torch::Tensor layer_weights_packed,
+             torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor k_cache, torch::Tensor v_cache,
+             torch::Tensor hidden, int num_layers, int start_position, int max_seq_len, float attn_scale) {
+  check_dev(ids, "ids", torch::kInt32);
+  const int64_t n = ids.numel();
+  TORCH_CHECK(n >= 1, "prefill needs at least one id");
+  TORCH_CHECK(start_position >= 0 && start_position + n <= max_seq_len, "positions [", start_position, ", ",
+              start_position + n, ") exceed max_seq_len ", max_seq_len);
+  check_dev(embed_weight, "embed_weight", torch::kHalf, V * H);
+  TORCH_CHECK(layer_weights_packed.is_cuda() && layer_weights_packed.scalar_type() == torch::kLong,
+              "layer_weights_packed must be an int64 GPU tensor");
+  TORCH_CHECK(layer_weights_packed.numel() >= (int64_t)num_layers * 12, "layer_weights_packed too small");
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(layer_weights_packed.data_ptr()) % 16 == 0,
+              "layer_weights_packed must be 16-byte aligned");
+  check_dev(cos_table, "cos_table", torch::kHalf, (int64_t)max_seq_len * HD);
+  check_dev(sin_table, "sin_table", torch::kHalf, (int64_t)max_seq_len * HD);
+  check_dev(k_cache, "k_cache", torch::kHalf, (int64_t)num_layers * NKV * max_seq_len * HD);
+  check_dev(v_cache, "v_cache", torch::kHalf, (int64_t)num_layers * NKV * max_seq_len * HD);
+  check_dev(hidden, "hidden", torch::kHalf, H);
+  check_rc(qwen_prefill(ids.data_ptr<int>(), (int)n, embed_weight.data_ptr(),
+                        reinterpret_cast<const LDGLayerWeight*>(layer_weights_packed.data_ptr()),
+                        cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                        hidden.data_ptr(), num_layers, start_position, max_seq_len, attn_scale, stream_of(ids)),
+           "prefill");
+}
+
 torch::Tensor lm_head_argmax(torch::Tensor hidden, torch::Tensor weight, c10::optional<torch::Tensor> logits_out) {
   check_dev(hidden, "hidden", torch::kHalf, H);
   check_dev(weight, "weight", torch::kHalf, V * H);
@@ -256,6 +283,11 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
   m.def("lm_head_argmax", &lm_head_argmax, "isolated lm_head GEMV + argmax", pybind11::arg("hidden"),
         pybind11::arg("weight"), pybind11::arg("logits_out") = pybind11::none());
   m.def("mlp_block", &mlp_block, "isolated RMSNorm + SwiGLU MLP + residual");
+  m.def("prefill", &prefill, "batched prefill of a prompt (MFMA): writes K/V of every position and hidden",
+        pybind11::arg("ids"), pybind11::arg("embed_weight"), pybind11::arg("layer_weights_packed"),
+        pybind11::arg("cos_table"), pybind11::arg("sin_table"), pybind11::arg("k_cache"), pybind11::arg("v_cache"),
+        pybind11::arg("hidden"), pybind11::arg("num_layers"), pybind11::arg("start_position"),
+        pybind11::arg("max_seq_len"), pybind11::arg("attn_scale"));
   m.def("last_error", &last_error, "synchronize and return the device-side error state (0 = ok)");
   m.def("set_trace", &set_trace, "record per-stage device timestamps of one token into an int64 GPU tensor "
         "[256, fins, events] (None to stop)", pybind11::arg("buf"), pybind11::arg("token") = 0);

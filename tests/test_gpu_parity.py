@@ -219,6 +219,72 @@ def _lib():
     return lib
 
 
+def _prefill(ext, run, ids, start):
+    w = run.w
+    f = torch.tensor(ids, dtype=torch.int32, device="cuda")
+    ext.prefill(f, w["embed_weight"], run.packed, w["cos_table"], w["sin_table"], run.kc, run.vc, run.hidden,
+                run.L, start, MAX_SEQ, SCALE)
+    torch.cuda.synchronize()
+    assert ext.last_error() == 0
+
+
+@pytest.mark.parametrize("n", [16, 128])
+def test_batched_prefill_matches_oracle(ext, rn, n):
+    """Batched (MFMA) prefill of an n-id prompt on the rn model (non-unit norms, untied
+    lm_head), 28 layers: the K/V cache of all n - 1 prefilled positions and the prefill's
+    hidden state (position n - 2) against one oracle forward; then the decode step of the
+    last id on that cache: greedy token (near-ties exempt), logits and hidden state."""
+    hw, w, packed = rn
+    ids = qw.synthetic_prompt(n, seed=50 + n)
+    oracle = orc.Oracle(hw)
+    ref = oracle.forward(ids, logits_at=[n - 1])
+    run = Run(w, packed, 28)
+    _prefill(ext, run, ids[:-1], 0)
+    dh0 = float((run.hidden.float().cpu() - ref["hidden"][n - 2]).abs().max())
+    kc = run.kc[:, :, : n - 1].float().cpu()
+    vc = run.vc[:, :, : n - 1].float().cpu()
+    dk = float((kc - oracle.k_cache[:, :, : n - 1]).abs().max())
+    dv = float((vc - oracle.v_cache[:, :, : n - 1]).abs().max())
+    toks, logits, hidden = run.forced(ext, ids[-1:], n - 1)
+    dl = float((logits[0] - ref["logits"][0]).abs().max())
+    dh = float((hidden[0] - ref["hidden"][n - 1]).abs().max())
+    gap = orc.top2_gap(ref["logits"][0])
+    print(f"prefill n={n}: K {dk:.3e} V {dv:.3e} hidden(prefill) {dh0:.3e}; next step logits {dl:.3e} "
+          f"hidden {dh:.3e} gap {gap:.3e}")
+    assert dk < 2e-2 and dv < 2e-2
+    assert dh0 <= TOL_HIDDEN and dh <= TOL_HIDDEN and dl <= TOL_LOGITS
+    if gap >= GAP_EXEMPT:
+        assert toks[0] == ref["tokens"][0]
+
+
+def test_batched_prefill_chunked_equals_whole(ext, full):
+    """Prefilling 200 ids as 77 + 123 (the second chunk at position 77, attending to the
+    first chunk's cache) gives the same K/V cache, bit for bit, as one prefill of all 200:
+    every position's arithmetic is the same in both, whatever tile or query block it lands
+    in."""
+    hw, w, packed = full
+    ids = qw.synthetic_prompt(200, seed=61)
+    a, b = Run(w, packed, 28), Run(w, packed, 28)
+    _prefill(ext, a, ids, 0)
+    _prefill(ext, b, ids[:77], 0)
+    _prefill(ext, b, ids[77:], 77)
+    assert torch.equal(a.kc, b.kc) and torch.equal(a.vc, b.vc)
+    assert torch.equal(a.hidden, b.hidden)
+
+
+def test_batched_prefill_bad_id_reported(ext, full):
+    """An id outside the vocabulary inside a device id tensor is reported by last_error()
+    as QWEN_ERR_BAD_TOKEN (5), and the next prefill works."""
+    hw, w, packed = full
+    run = Run(w, packed, 2)
+    f = torch.tensor([5, V, 7], dtype=torch.int32, device="cuda")
+    ext.prefill(f, w["embed_weight"], packed, w["cos_table"], w["sin_table"], run.kc, run.vc, run.hidden, 2, 0,
+                MAX_SEQ, SCALE)
+    torch.cuda.synchronize()
+    assert ext.last_error() == 5
+    _prefill(ext, run, [5, 6, 7], 0)
+
+
 def test_decode_persistent_c_abi(ext, full, qa):
     """launch_ldg_decode_persistent through the C-ABI (ctypes, the reference's 27-argument
     order with cache_len), on torch's current stream: the same token, K/V row and hidden

@@ -85,6 +85,12 @@ class OracleStub(types.ModuleType):
         out = [self.oracle.step(ids[s], start + s)["token"] for s in range(n)]
         return torch.tensor(out, dtype=torch.int32)
 
+    def prefill(self, ids, *args):
+        num_layers, start, max_seq, scale = args[-4:]
+        ids = ids.tolist()
+        self.calls.append(("prefill", start, len(ids)))
+        self.oracle.forward(ids, start=start)
+
 
 @pytest.fixture(scope="module")
 def small_hw():
@@ -162,9 +168,28 @@ def test_generate_ids_prefill_then_nosync(qa_cpu, small_hw):
     out = dec.generate_ids(prompt, 6)
     ref = orc.Oracle(small_hw).greedy(prompt, 6)
     assert out == ref["tokens"]
-    # prefill covers positions 0..n-2 in one launch, generation starts at n-1
-    assert stub.calls == [("generate_ex", 3, 0, 4), ("generate_nosync", 5, 4, 6)]
+    # prefill covers positions 0..n-2 in one batched launch, generation starts at n-1
+    assert stub.calls == [("prefill", 0, 4), ("generate_nosync", 5, 4, 6)]
     assert dec.position == len(prompt) - 1 + 6
+
+
+def test_prefill_returns_token_after_prompt(qa_cpu, small_hw):
+    """prefill(ids): the batched launch over ids[:-1], then one decode step of ids[-1]
+    whose greedy token is returned; batched=False teacher forces every id instead."""
+    mod, stub = qa_cpu
+    prompt = [7, 2, 9, 4, 4, 1]
+    ref = orc.Oracle(small_hw).greedy(prompt, 1)["tokens"][0]
+    dec = mod.Decoder(weights=_weights(mod), verbose=False)
+    stub.calls.clear()
+    assert dec.prefill(prompt) == ref
+    assert stub.calls == [("prefill", 0, 5), ("generate_ex", 1, 5, 1)]
+    assert dec.position == len(prompt)
+    stub.oracle.reset()
+    dec.reset()
+    stub.calls.clear()
+    assert dec.prefill(prompt, batched=False) == ref
+    assert stub.calls == [("generate_ex", 7, 0, 6)]
+    assert dec.position == len(prompt)
 
 
 def test_generate_text_truncates_at_eos(qa_cpu, small_hw):
