@@ -246,6 +246,17 @@ def run_prefill(args):
     ms = _median(ts)
     flops = prefill_flops(PREFILL)
     tflops = flops / (ms / 1e3) / 1e12
+    # per-phase times of the last launch from its grid-barrier timestamps (100 MHz ticks)
+    stamps = qa.qwen_megakernel_C.prefill_timestamps()
+    names = ["qkv", "attention", "o_proj", "gate_up", "down"]
+    per = {k: [] for k in names}
+    for layer in range(28):
+        for k, name in enumerate(names):
+            i = 2 + 5 * layer + k
+            per[name].append((stamps[i] - stamps[i - 1]) / 100.0)
+    phases = {name: round(sum(v) / len(v), 2) for name, v in per.items()}
+    phases["embedding"] = round((stamps[1] - stamps[0]) / 100.0, 2)
+    log(f"prefill phase means over layers (us): {phases}")
     return {
         "metric": f"batched prefill tokens/sec ({PREFILL}-id prompt, 28 layers, one launch)",
         "value": round(PREFILL / ms * 1e3, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -255,6 +266,7 @@ def run_prefill(args):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
                      "kernel": "pf::qwen_prefill_kernel", "flops_per_launch": flops, "kernel_ms": round(ms, 4)},
+        "phases_us_per_layer": phases,
         "cpu_baseline": None,
     }
 

@@ -171,6 +171,13 @@ int qwen_prefill(
     int num_layers, int start_position, int max_seq_len, float attn_scale,
     hipStream_t stream);
 
+/* Profiling aid for qwen_prefill: the wall-clock times (s_memrealtime ticks,
+ * 100 MHz) at which the last prefill on the current device started and passed
+ * each of its grid barriers: [0] start, [1] after the embedding, then for each
+ * layer the ends of its QKV, attention, o_proj, gate/up and down phases. Copies
+ * min(max_entries, 2 + 5 * 28) entries to host memory `out`. */
+int qwen_prefill_timestamps(unsigned long long* out, int max_entries);
+
 /* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */

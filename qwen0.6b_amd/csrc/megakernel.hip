@@ -312,7 +312,10 @@ constexpr long PF_Q = PF_X + (long)MAX_SEQ_LIMIT * HIDDEN * 4;
 constexpr long PF_AO = PF_Q + (long)MAX_SEQ_LIMIT * QSZ * 2;
 constexpr long PF_IM = PF_AO + (long)MAX_SEQ_LIMIT * QSZ * 2;
 constexpr long PF_BAR = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
-constexpr long PF_BYTES = PF_BAR + 256;
+constexpr int PF_NTS = 1 + 1 + 5 * MAX_LAYERS;  // launch start, then every grid barrier
+constexpr long PF_BAR_BYTES = 4096;  // barrier counters and flags, one 128-byte line each
+constexpr long PF_TS = PF_BAR + PF_BAR_BYTES;
+constexpr long PF_BYTES = PF_TS + 8L * ((PF_NTS + 31) / 32 * 32);
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
@@ -498,6 +501,7 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.AO = (_Float16*)(st->pf + PF_AO);
   P.IM = (_Float16*)(st->pf + PF_IM);
   P.bar = (u32*)(st->pf + PF_BAR);
+  P.ts = (u64*)(st->pf + PF_TS);
   P.status = st->heap.status;
   P.deadline = st->deadline;
   P.n = n;
@@ -505,10 +509,27 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.num_layers = num_layers;
   P.max_seq = max_seq_len;
   P.attn_scale = attn_scale;
-  if (zero_words(P.bar, 256, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
+  if (zero_words(P.bar, PF_BAR_BYTES, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
   void* args[] = {&P};
   if (hipLaunchCooperativeKernel((const void*)pf::qwen_prefill_kernel, dim3(NWG), dim3(pf::NT), args, 0, stream) !=
       hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  return QWEN_OK;
+}
+
+extern "C" int qwen_prefill_timestamps(unsigned long long* out, int max_entries) {
+  if (!out || max_entries < 1) return QWEN_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceState* st = nullptr;
+  int rc = device_state(&st);
+  if (rc != QWEN_OK) return rc;
+  const int n = max_entries < PF_NTS ? max_entries : PF_NTS;
+  if (!st->pf) {
+    memset(out, 0, sizeof(unsigned long long) * n);
+    return QWEN_OK;
+  }
+  if (hipDeviceSynchronize() != hipSuccess) return QWEN_ERR_LAUNCH;
+  if (hipMemcpy(out, st->pf + PF_TS, sizeof(unsigned long long) * n, hipMemcpyDeviceToHost) != hipSuccess)
     return QWEN_ERR_LAUNCH;
   return QWEN_OK;
 }

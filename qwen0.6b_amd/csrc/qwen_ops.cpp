@@ -14,6 +14,7 @@
 #include <cstdint>
 #include <string>
 #include <tuple>
+#include <vector>
 
 #include "qwen_megakernel.h"
 
@@ -215,6 +216,13 @@ void prefill(torch::Tensor ids, torch::Tensor embed_weight, torch::Tensor layer_
            "prefill");
 }
 
+// wall-clock ticks at the start and every grid barrier of the last prefill (profiling aid)
+std::vector<int64_t> prefill_timestamps() {
+  std::vector<unsigned long long> buf(2 + 5 * 28);
+  check_rc(qwen_prefill_timestamps(buf.data(), (int)buf.size()), "prefill_timestamps");
+  return std::vector<int64_t>(buf.begin(), buf.end());
+}
+
 torch::Tensor lm_head_argmax(torch::Tensor hidden, torch::Tensor weight, c10::optional<torch::Tensor> logits_out) {
   check_dev(hidden, "hidden", torch::kHalf, H);
   check_dev(weight, "weight", torch::kHalf, V * H);
@@ -283,6 +291,8 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
   m.def("lm_head_argmax", &lm_head_argmax, "isolated lm_head GEMV + argmax", pybind11::arg("hidden"),
         pybind11::arg("weight"), pybind11::arg("logits_out") = pybind11::none());
   m.def("mlp_block", &mlp_block, "isolated RMSNorm + SwiGLU MLP + residual");
+  m.def("prefill_timestamps", &prefill_timestamps, "wall-clock ticks (100 MHz) at the start and at every grid "
+        "barrier of the last prefill: start, embedding, then QKV / attention / o_proj / gate-up / down per layer");
   m.def("prefill", &prefill, "batched prefill of a prompt (MFMA): writes K/V of every position and hidden",
         pybind11::arg("ids"), pybind11::arg("embed_weight"), pybind11::arg("layer_weights_packed"),
         pybind11::arg("cos_table"), pybind11::arg("sin_table"), pybind11::arg("k_cache"), pybind11::arg("v_cache"),
