@@ -85,7 +85,13 @@ def cpu_baseline(hw, budget_s=12.0, max_steps=400):
         tok = oracle.step(tok, PREFILL + 1 + n)["token"]
         n += 1
     dt = time.perf_counter() - t0
-    return dict(value=round(n / dt, 3), unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(value=round(n / dt, 3), unit="tokens/s", cores=torch.get_num_threads(), cpu=cpu, kind="port",
                 sample=f"{n} greedy decode steps of the fp32 oracle at positions {PREFILL + 1}..{PREFILL + n} "
                        f"(28 layers + lm_head, random KV history), {dt:.1f} s")
 
@@ -204,6 +210,40 @@ def run_mlp(args):
     return aux_line("isolated MLP block (C2): microseconds per call", round(ms * 1e3, 2), "us/call", False, "c2",
                     {"hidden": 1024, "inter": 3072, "weight_sets": 16}, "fast::qwen_decode_kernel", nbytes, ms,
                     args.steps, args.warmup)
+
+
+STAGES = ["qkv", "attention", "combine", "o_proj", "o_sum", "gate_up", "down", "down_sum"]
+
+
+def trace_breakdown(tr, layers=28):
+    """Per-stage times of one traced token (tr: [256 workgroups, 8 * layers + 1, events] of
+    100 MHz ticks; event 0 = starts waiting, 1 = has its input, 3 = stored and acknowledged),
+    means over layers 1 .. layers - 1: 'hop' from the previous stage's last store to this
+    stage's last input, 'proc' from the last input to the last store, and the grouping
+    GEMV (qkv, o_proj, gate_up, down) / attention (attention, combine) / residual sums."""
+    import numpy as np
+
+    t = (tr.astype(np.int64) - tr[:, 0, 0].min()) / 100.0
+    lines = ["stage       hop_us  proc_us  stage_us"]
+    per = {}
+    for st, name in enumerate(STAGES):
+        hop, proc, dur = [], [], []
+        for layer in range(1, layers):
+            s = 8 * layer + st
+            last_prev = t[:, s - 1, 3].max()
+            hop.append(t[:, s, 1].max() - last_prev)
+            proc.append(t[:, s, 3].max() - t[:, s, 1].max())
+            dur.append(t[:, s, 3].max() - last_prev)
+        per[name] = float(np.mean(dur))
+        lines.append(f"{name:10s} {np.mean(hop):7.2f} {np.mean(proc):8.2f} {np.mean(dur):9.2f}")
+    layer = np.mean([t[:, 8 * l + 7, 3].max() - t[:, 8 * l - 1, 3].max() for l in range(1, layers)])
+    lm = t[:, 8 * layers, 3].max() - t[:, 8 * layers - 1, 3].max()
+    token = t[:, 8 * layers, 3].max()
+    gemv = per["qkv"] + per["o_proj"] + per["gate_up"] + per["down"]
+    lines.append(f"layer {layer:.2f} us (GEMV stages {gemv:.2f}, attention {per['attention'] + per['combine']:.2f}, "
+                 f"residual sums {per['o_sum'] + per['down_sum']:.2f}); lm_head + argmax {lm:.2f} us; "
+                 f"token {token:.2f} us (traced build)")
+    return "\n".join(lines)
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
@@ -384,8 +424,10 @@ def main():
         one_step()
         torch.cuda.synchronize()
         ext.set_trace(None, 0)
-        np.save(args.trace, buf.view(256, fins, ext.trace_events()).cpu().numpy())
+        tr = buf.view(256, fins, ext.trace_events()).cpu().numpy()
+        np.save(args.trace, tr)
         log(f"trace written to {args.trace}")
+        log(trace_breakdown(tr))
 
     if args.copy_calibration:
         src = torch.empty(1 << 29, dtype=torch.float16, device="cuda").fill_(1.0)
