@@ -178,6 +178,42 @@ int qwen_prefill(
  * min(max_entries, 2 + 5 * 28) entries to host memory `out`. */
 int qwen_prefill_timestamps(unsigned long long* out, int max_entries);
 
+/* Token sampling (no counterpart in the reference, which decodes greedily:
+ * Model/Qwen06B_architecture.py:343-382). One token from fp32 logits[n] into
+ * *out_token (device int32): temperature <= 0 or top_k == 1 gives the argmax
+ * (lowest index on ties); otherwise the logits are scaled by 1/temperature,
+ * top_k > 0 keeps the tokens whose logit is >= the k-th largest (ties kept),
+ * top_p < 1 then keeps the most probable of those until the mass strictly
+ * above a token reaches top_p of the kept mass (the boundary token and its
+ * ties kept), and the token is drawn from the renormalised softmax over the
+ * kept set by a Gumbel-max pick whose noise for token j is Philox4x32-10 of
+ * counter (j, step, 0, 0) under key (seed low, seed high) words: the same
+ * (logits, parameters, seed, step) always give the same token. NaN logits are
+ * never drawn. */
+int qwen_sample(const float* logits, int n, float temperature, int top_k, float top_p,
+                unsigned long long seed, unsigned int step, int* out_token, hipStream_t stream);
+
+/* Sampled generation (no counterpart in the reference): generate_nosync whose
+ * every next token comes from qwen_sample over that step's logits (seed,
+ * step = the position of the step's input token) instead of the argmax. Runs
+ * as num_steps pairs of launches (a decode step, then the sampler) with no
+ * host synchronisation. With eos_token_id >= 0 the generation ends after the
+ * first sampled eos: output_log[0 .. n) holds the sampled ids, eos last when it
+ * was reached, later entries are -1, and n = *out_count (device int32,
+ * nullable) <= num_steps; the K/V cache holds positions start_position ..
+ * start_position + n - 1. The launches after the eos still run (the host
+ * enqueued them) and their results mean nothing: K/V entries past that
+ * range, hidden_buffer and g_normalized; a caller that expects an early eos
+ * enqueues shorter runs. Allocates a 610 KB per-device buffer on first use. */
+int qwen_generate_sampled(
+    int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
+    const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+    const void* lm_head_weight, const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache, void* hidden_buffer, void* g_normalized,
+    int* output_log, int* out_count, int num_layers, int start_position,
+    int max_seq_len, float attn_scale, float temperature, int top_k, float top_p,
+    unsigned long long seed, hipStream_t stream);
+
 /* Isolated lm_head + argmax: *out_token = argmax_r (W[r,:] . h), h fp16 [1024]
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */

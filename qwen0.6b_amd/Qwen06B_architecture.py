@@ -48,6 +48,10 @@ DEVICE = "cuda"  # where Decoder allocates its state; the engine itself needs th
 _OPS = ("decode", "generate_nosync", "generate_until")
 
 
+# sampled generation with an eos id: steps enqueued between two host checks for the eos
+SAMPLED_CHUNK = 32
+
+
 def _require_megakernel_op(op_name: str):
     """Return an op from the extension module or the torch.ops namespace."""
     if qwen_megakernel_C is not None and hasattr(qwen_megakernel_C, op_name):
@@ -364,30 +368,71 @@ class Decoder:
         self._position += n
         return out[:n].cpu().tolist()
 
-    def generate_ids(self, ids, max_tokens: int = 100, eos_token_id=None) -> list:
-        """Greedy generation on token ids (reference ``generate`` without the tokenizer):
-        prefill ids[:-1], then ``max_tokens`` on-device steps from ids[-1]; with
-        ``eos_token_id`` the device stops after that id (which ends the list)."""
+    def generate_sampled(self, first_token_id: int, max_tokens: int, temperature: float, top_k: int = 0,
+                         top_p: float = 1.0, seed: int = 0, eos_token_id=None) -> list:
+        """Up to ``max_tokens`` sampled steps from the current position, with no host
+        synchronisation until the end: each step's next token is drawn on the device from
+        its logits (temperature, then top-k, then top-p, then a draw seeded by ``seed`` and
+        the step's position; temperature <= 0 or top_k == 1 is greedy). With
+        ``eos_token_id`` the generation ends after that id (which ends the list), checked
+        on the host every ``SAMPLED_CHUNK`` steps (the steps enqueued after an eos are
+        wasted work); advances the position by the number of steps run."""
+        if self._position + max_tokens > MAX_SEQ_LEN:
+            raise RuntimeError(f"positions {self._position}..{self._position + max_tokens} exceed {MAX_SEQ_LEN}")
+        if top_k < 0 or not 0.0 <= top_p or temperature != temperature:
+            raise ValueError(f"invalid sampling parameters temperature={temperature} top_k={top_k} top_p={top_p}")
+        gen = _require_megakernel_op("generate_sampled")
+        eos = -1 if eos_token_id is None else int(eos_token_id)
+        chunk = max_tokens if eos < 0 else SAMPLED_CHUNK
+        out, first = [], int(first_token_id)
+        while len(out) < max_tokens:
+            m = min(chunk, max_tokens - len(out))
+            ids, count = gen(first, m, eos, self._embed_weight, self._layer_weights_packed, self._final_norm_weight,
+                             self._lm_head_weight, self._cos_table, self._sin_table, self._k_cache, self._v_cache,
+                             self._hidden, self._norm_out, self._num_layers, self._position, MAX_SEQ_LEN,
+                             self._attn_scale, float(temperature), int(top_k), float(top_p),
+                             int(seed) & 0xFFFFFFFFFFFFFFFF)
+            n = int(count.item())
+            _check_device_errors()
+            self._position += n
+            out += ids[:n].cpu().tolist()
+            if n < m or out[-1] == eos:
+                break
+            first = out[-1]
+        return out
+
+    def generate_ids(self, ids, max_tokens: int = 100, eos_token_id=None, temperature: float = 0.0,
+                     top_k: int = 0, top_p: float = 1.0, seed: int = 0) -> list:
+        """Generation on token ids (reference ``generate`` without the tokenizer): prefill
+        ids[:-1], then ``max_tokens`` on-device steps from ids[-1]; with ``eos_token_id``
+        the device stops after that id (which ends the list). Greedy by default, as the
+        reference; ``temperature`` > 0 samples (see ``generate_sampled``)."""
         self.reset()
         ids = [int(t) for t in ids]
         self._prefill_kv(ids[:-1])
+        if temperature > 0 and top_k != 1:
+            return self.generate_sampled(ids[-1], max_tokens, temperature, top_k, top_p, seed, eos_token_id)
         if eos_token_id is not None:
             return self.generate_until(ids[-1], max_tokens, eos_token_id)
         out = self.generate_nosync(ids[-1], max_tokens).cpu().tolist()
         _check_device_errors()
         return out
 
-    def generate(self, prompt: str, max_tokens: int = 100) -> str:
+    def generate(self, prompt: str, max_tokens: int = 100, temperature: float = 0.0, top_k: int = 0,
+                 top_p: float = 1.0, seed: int = 0) -> str:
         if self.tokenizer is None:
             raise RuntimeError("generate(prompt) needs a tokenizer; use generate_ids() for token ids")
         ids = self.tokenizer.encode(prompt, add_special_tokens=True)
         eos = self.tokenizer.eos_token_id
-        out = self.generate_ids(ids, max_tokens, eos_token_id=eos)
+        out = self.generate_ids(ids, max_tokens, eos_token_id=eos, temperature=temperature, top_k=top_k,
+                                top_p=top_p, seed=seed)
         if eos in out:
             out = out[: out.index(eos)]
         return self.tokenizer.decode(out, skip_special_tokens=True)
 
 
-def generate(prompt: str, max_tokens: int = 50, verbose: bool = True, model_name="Qwen/Qwen3-0.6B") -> str:
-    """One-shot convenience: load model, generate, return text."""
-    return Decoder(model_name=model_name, verbose=verbose).generate(prompt, max_tokens)
+def generate(prompt: str, max_tokens: int = 50, verbose: bool = True, model_name="Qwen/Qwen3-0.6B",
+             temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0, seed: int = 0) -> str:
+    """One-shot convenience: load model, generate (greedy unless temperature > 0), return text."""
+    return Decoder(model_name=model_name, verbose=verbose).generate(prompt, max_tokens, temperature, top_k,
+                                                                    top_p, seed)

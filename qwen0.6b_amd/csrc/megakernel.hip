@@ -121,6 +121,9 @@ constexpr bool kTrace = true;
 // the batched prefill kernel (namespace pf)
 #include "prefill_body.inc"
 
+// the token sampler (namespace smp)
+#include "sample_body.inc"
+
 // one workgroup per CU, as the decode kernel: each records the XCC it runs on
 __global__ void __launch_bounds__(BLOCK, 1) qwen_placement_probe(u32* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
@@ -160,6 +163,7 @@ struct DeviceState {
   Workspace fixed;                // the `scratch` array of this device (no allocation)
   LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
   char* pf = nullptr;             // prefill activations (PF_BYTES), on first use
+  char* smp = nullptr;            // sampled generation: one step's logits and token (SMP_BYTES)
   u64 clk_khz = 100000;
   u64 deadline = 0;
   u64* trace = nullptr;
@@ -177,12 +181,13 @@ void teardown() {
   std::lock_guard<std::mutex> lock(g_mu);
   for (int d = 0; d < MAX_DEVICES; ++d) {
     DeviceState& st = g_dev[d];
-    if (!st.heap.ws && !st.tab && !st.pf) continue;
+    if (!st.heap.ws && !st.tab && !st.pf && !st.smp) continue;
     if (hipSetDevice(d) != hipSuccess) continue;
     (void)hipDeviceSynchronize();
     if (st.heap.ws) (void)hipFree(st.heap.ws);
     if (st.tab) (void)hipFree(st.tab);
     if (st.pf) (void)hipFree(st.pf);
+    if (st.smp) (void)hipFree(st.smp);
     st = DeviceState();
   }
 }
@@ -317,7 +322,25 @@ constexpr long PF_BAR_BYTES = 4096;  // barrier counters and flags, one 128-byte
 constexpr long PF_TS = PF_BAR + PF_BAR_BYTES;
 constexpr long PF_BYTES = PF_TS + 8L * ((PF_NTS + 31) / 32 * 32);
 
+// sampled generation: one step's fp32 logits, the step's greedy id (unused), the sampled id, and
+// the embedding row of the sampled id (the next decode step's one-row embedding table)
+constexpr long SMP_LOGITS = 0;
+constexpr long SMP_ARGMAX = SMP_LOGITS + (long)VOCAB * 4;
+constexpr long SMP_TOKEN = SMP_ARGMAX + 256;
+constexpr long SMP_ROW = SMP_TOKEN + 256;
+constexpr long SMP_BYTES = SMP_ROW + HIDDEN * 2;
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// temperature, top_k and top_p as the sampler reads them (NaN refused)
+bool sample_args_ok(float temperature, int top_k, float top_p) {
+  return temperature == temperature && top_k >= 0 && top_p == top_p;
+}
+
+int launch_sampler(const smp::SParams& S, hipStream_t stream) {
+  hipLaunchKernelGGL(smp::qwen_sample_kernel, dim3(1), dim3(smp::NT), 0, stream, S);
+  return hipGetLastError() == hipSuccess ? QWEN_OK : QWEN_ERR_LAUNCH;
+}
 
 int fill_decode(KParams& P, const void* embed, const LDGLayerWeight* lw, const void* fnorm, const void* lm_head,
                 const void* cos_t, const void* sin_t, void* kc, void* vc, void* hidden, void* norm_out,
@@ -531,6 +554,87 @@ extern "C" int qwen_prefill_timestamps(unsigned long long* out, int max_entries)
   if (hipDeviceSynchronize() != hipSuccess) return QWEN_ERR_LAUNCH;
   if (hipMemcpy(out, st->pf + PF_TS, sizeof(unsigned long long) * n, hipMemcpyDeviceToHost) != hipSuccess)
     return QWEN_ERR_LAUNCH;
+  return QWEN_OK;
+}
+
+extern "C" int qwen_sample(const float* logits, int n, float temperature, int top_k, float top_p,
+                           unsigned long long seed, unsigned int step, int* out_token, hipStream_t stream) {
+  if (!logits || !out_token || n < 1 || !sample_args_ok(temperature, top_k, top_p)) return QWEN_ERR_ARG;
+  smp::SParams S;
+  memset(&S, 0, sizeof(S));
+  S.logits = logits;
+  S.n = n;
+  S.temperature = temperature;
+  S.top_k = top_k;
+  S.top_p = top_p;
+  S.seed = seed;
+  S.step = step;
+  S.out_token = out_token;
+  S.eos = -1;
+  return launch_sampler(S, stream);
+}
+
+extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
+                                     const LDGLayerWeight* layer_weights, const void* final_norm_weight,
+                                     const void* lm_head_weight, const void* cos_table, const void* sin_table,
+                                     void* k_cache, void* v_cache, void* hidden_buffer, void* g_normalized,
+                                     int* output_log, int* out_count, int num_layers, int start_position,
+                                     int max_seq_len, float attn_scale, float temperature, int top_k, float top_p,
+                                     unsigned long long seed, hipStream_t stream) {
+  KParams P;
+  // the whole range is checked before anything is launched
+  int rc = fill_decode(P, embed_weight, layer_weights, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                       k_cache, v_cache, hidden_buffer, g_normalized, num_layers, start_position, num_steps,
+                       max_seq_len, attn_scale);
+  if (rc != QWEN_OK) return rc;
+  if (!output_log || first_token_id < 0 || first_token_id >= VOCAB || eos_token_id < -1 || eos_token_id >= VOCAB ||
+      !sample_args_ok(temperature, top_k, top_p))
+    return QWEN_ERR_ARG;
+  char* buf = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState* st = nullptr;
+    if ((rc = device_state(&st)) != QWEN_OK) return rc;
+    if (!st->smp) {
+      void* p = nullptr;
+      if (hipMalloc(&p, SMP_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+      st->smp = (char*)p;
+    }
+    buf = st->smp;
+  }
+  float* logits = (float*)(buf + SMP_LOGITS);
+  int* tok = (int*)(buf + SMP_TOKEN);
+  _Float16* row = (_Float16*)(buf + SMP_ROW);
+  smp::SParams S;
+  memset(&S, 0, sizeof(S));
+  S.logits = logits;
+  S.n = VOCAB;
+  S.temperature = temperature;
+  S.top_k = top_k;
+  S.top_p = top_p;
+  S.seed = seed;
+  S.out_token = tok;
+  S.eos = eos_token_id;
+  S.out_count = out_count;
+  S.embed = (const _Float16*)embed_weight;
+  S.row = row;
+  // Per step: one decode launch writing the step's logits, then the sampler. The host never
+  // waits, so the decode step cannot take its input id as an argument: from step 1 on its
+  // embedding table is the one row the sampler copied out for the id it drew (input id 0).
+  for (int s = 0; s < num_steps; ++s) {
+    if ((rc = fill_decode(P, s == 0 ? embed_weight : (const void*)row, layer_weights, final_norm_weight,
+                          lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized,
+                          num_layers, start_position + s, 1, max_seq_len, attn_scale)) != QWEN_OK)
+      return rc;
+    P.first_token = s == 0 ? first_token_id : 0;
+    P.out_tokens = (int*)(buf + SMP_ARGMAX);
+    P.logits_out = logits;
+    if ((rc = launch(P, stream)) != QWEN_OK) return rc;
+    S.step = (u32)(start_position + s);
+    S.out_log = output_log + s;
+    S.index = s;
+    if ((rc = launch_sampler(S, stream)) != QWEN_OK) return rc;
+  }
   return QWEN_OK;
 }
 

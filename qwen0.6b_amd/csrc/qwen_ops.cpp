@@ -189,6 +189,46 @@ std::tuple<torch::Tensor, torch::Tensor> generate_until(int first_token_id, int 
   return {out, count};
 }
 
+// one token sampled from fp32 logits (device int32[1])
+torch::Tensor sample(torch::Tensor logits, double temperature, int64_t top_k, double top_p, uint64_t seed,
+                     int64_t step) {
+  check_dev(logits, "logits", torch::kFloat);
+  TORCH_CHECK(logits.numel() >= 1 && logits.numel() <= INT32_MAX, "logits must hold 1 .. 2^31-1 values");
+  TORCH_CHECK(top_k >= 0 && top_k <= INT32_MAX, "top_k must be >= 0");
+  TORCH_CHECK(step >= 0 && step <= UINT32_MAX, "step must fit 32 bits");
+  auto out = torch::empty({1}, torch::dtype(torch::kInt32).device(logits.device()));
+  check_rc(qwen_sample(logits.data_ptr<float>(), (int)logits.numel(), (float)temperature, (int)top_k, (float)top_p,
+                       seed, (unsigned)step, out.data_ptr<int>(), stream_of(logits)),
+           "sample");
+  return out;
+}
+
+// generate_until with sampling; returns (ids int32[num_steps], count int32[1]) on the device
+std::tuple<torch::Tensor, torch::Tensor> generate_sampled(
+    int first_token_id, int num_steps, int eos_token_id, torch::Tensor embed_weight,
+    torch::Tensor layer_weights_packed, torch::Tensor final_norm_weight, torch::Tensor lm_head_weight,
+    torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor k_cache, torch::Tensor v_cache,
+    torch::Tensor hidden, torch::Tensor norm_out, int num_layers, int start_position, int max_seq_len,
+    float attn_scale, double temperature, int64_t top_k, double top_p, uint64_t seed) {
+  const LDGLayerWeight* tab = check_common(embed_weight, layer_weights_packed, final_norm_weight, lm_head_weight,
+                                           cos_table, sin_table, k_cache, v_cache, hidden, norm_out, num_layers,
+                                           max_seq_len);
+  TORCH_CHECK(first_token_id >= 0 && first_token_id < V, "first_token_id ", first_token_id, " out of range");
+  TORCH_CHECK(eos_token_id >= -1 && eos_token_id < V, "eos_token_id ", eos_token_id, " out of range");
+  TORCH_CHECK(num_steps >= 1, "num_steps must be >= 1");
+  TORCH_CHECK(start_position >= 0 && (int64_t)start_position + num_steps <= max_seq_len, "positions exceed max_seq_len");
+  TORCH_CHECK(top_k >= 0 && top_k <= INT32_MAX, "top_k must be >= 0");
+  auto out = torch::full({num_steps}, -1, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  auto count = torch::zeros({1}, torch::dtype(torch::kInt32).device(embed_weight.device()));
+  const int rc = qwen_generate_sampled(
+      first_token_id, num_steps, eos_token_id, embed_weight.data_ptr(), tab, final_norm_weight.data_ptr(),
+      lm_head_weight.data_ptr(), cos_table.data_ptr(), sin_table.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+      hidden.data_ptr(), norm_out.data_ptr(), out.data_ptr<int>(), count.data_ptr<int>(), num_layers, start_position,
+      max_seq_len, attn_scale, (float)temperature, (int)top_k, (float)top_p, seed, stream_of(embed_weight));
+  check_rc(rc, "generate_sampled");
+  return {out, count};
+}
+
 // batched prefill of `ids` (int32 device tensor) at start_position ..; writes K/V and hidden
 void prefill(torch::Tensor ids, torch::Tensor embed_weight, torch::Tensor layer_weights_packed,
              torch::Tensor cos_table, torch::Tensor sin_table, torch::Tensor k_cache, torch::Tensor v_cache,
@@ -298,6 +338,18 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
         pybind11::arg("cos_table"), pybind11::arg("sin_table"), pybind11::arg("k_cache"), pybind11::arg("v_cache"),
         pybind11::arg("hidden"), pybind11::arg("num_layers"), pybind11::arg("start_position"),
         pybind11::arg("max_seq_len"), pybind11::arg("attn_scale"));
+  m.def("sample", &sample, "one token from fp32 logits: temperature, top-k, top-p, Philox Gumbel-max draw",
+        pybind11::arg("logits"), pybind11::arg("temperature"), pybind11::arg("top_k") = 0,
+        pybind11::arg("top_p") = 1.0, pybind11::arg("seed") = 0, pybind11::arg("step") = 0);
+  m.def("generate_sampled", &generate_sampled, "on-device sampled generation (no host sync), ends at eos_token_id "
+        "(-1: never)",
+        pybind11::arg("first_token_id"), pybind11::arg("num_steps"), pybind11::arg("eos_token_id"),
+        pybind11::arg("embed_weight"), pybind11::arg("layer_weights_packed"), pybind11::arg("final_norm_weight"),
+        pybind11::arg("lm_head_weight"), pybind11::arg("cos_table"), pybind11::arg("sin_table"),
+        pybind11::arg("k_cache"), pybind11::arg("v_cache"), pybind11::arg("hidden"), pybind11::arg("norm_out"),
+        pybind11::arg("num_layers"), pybind11::arg("start_position"), pybind11::arg("max_seq_len"),
+        pybind11::arg("attn_scale"), pybind11::arg("temperature"), pybind11::arg("top_k"), pybind11::arg("top_p"),
+        pybind11::arg("seed"));
   m.def("last_error", &last_error, "synchronize and return the device-side error state (0 = ok)");
   m.def("set_trace", &set_trace, "record per-stage device timestamps of one token into an int64 GPU tensor "
         "[256, fins, events] (None to stop)", pybind11::arg("buf"), pybind11::arg("token") = 0);

@@ -55,7 +55,8 @@ def test_pybind_module_surface():
         pytest.skip("extension not built")
     assert m.abi_version() == 2
     for op in ("decode", "generate_nosync", "abi_version", "built_torch_version", "generate_ex",
-               "lm_head_argmax", "mlp_block", "last_error"):
+               "lm_head_argmax", "mlp_block", "last_error", "generate_until", "prefill", "prefill_timestamps",
+               "sample", "generate_sampled", "set_trace", "set_wait_deadline_us"):
         assert hasattr(m, op), op
     import torch
 

@@ -17,6 +17,7 @@ import torch
 
 import qwen_weights as qw
 from oracle import qwen3_oracle as orc
+from oracle import sampling as sp
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 MOD = os.path.join(REPO, "qwen0.6b_amd", "Qwen06B_architecture.py")
@@ -84,6 +85,19 @@ class OracleStub(types.ModuleType):
         ids = forced.tolist()
         out = [self.oracle.step(ids[s], start + s)["token"] for s in range(n)]
         return torch.tensor(out, dtype=torch.int32)
+
+    def generate_sampled(self, first, n, eos, *args):
+        num_layers, start, max_seq, scale, temperature, top_k, top_p, seed = args[-8:]
+        self.calls.append(("generate_sampled", first, start, n, eos))
+        out, tok = [], first
+        for s in range(n):
+            logits = self.oracle.step(tok, start + s)["logits"].numpy()
+            tok = sp.sample(logits, temperature, top_k, top_p, seed, start + s)
+            out.append(tok)
+            if tok == eos:
+                break
+        count = len(out)
+        return torch.tensor(out + [-1] * (n - count), dtype=torch.int32), torch.tensor([count], dtype=torch.int32)
 
     def prefill(self, ids, *args):
         num_layers, start, max_seq, scale = args[-4:]
@@ -220,6 +234,50 @@ def test_generate_ids_stops_at_eos(qa_cpu, small_hw):
     assert out == ref[:k + 1]
     assert stub.calls[-1] == ("generate_until", 5, 4, 8, ref[k])
     assert dec.position == len(prompt) - 1 + k + 1
+
+
+def _sampled_ref(hw, prompt, n, eos=None, **kw):
+    o = orc.Oracle(hw)
+    o.forward(prompt[:-1])
+    out, tok = [], prompt[-1]
+    for s in range(n):
+        pos = len(prompt) - 1 + s
+        tok = sp.sample(o.step(tok, pos)["logits"].numpy(), kw["temperature"], kw["top_k"], kw["top_p"],
+                        kw["seed"], pos)
+        out.append(tok)
+        if tok == eos:
+            break
+    return out
+
+
+def test_generate_ids_sampled_chunks_and_eos(qa_cpu, small_hw):
+    """temperature > 0 goes to generate_sampled; with an eos id the Decoder enqueues
+    SAMPLED_CHUNK steps at a time, continues from the last id and position, and stops
+    after the eos; the draws depend on the position only, so chunking changes nothing."""
+    mod, stub = qa_cpu
+    mod.SAMPLED_CHUNK = 3
+    kw = dict(temperature=1.3, top_k=20, top_p=0.9, seed=77)
+    prompt = [3, 1, 4, 1, 5]
+    ref = _sampled_ref(small_hw, prompt, 10, **kw)
+    dec = mod.Decoder(weights=_weights(mod), verbose=False)
+    assert dec.generate_ids(prompt, 10, **kw) == ref
+    assert stub.calls[-1] == ("generate_sampled", 5, 4, 10, -1)  # no eos: one launch sequence
+    k = next(i for i in range(4, 10) if ref[i] not in ref[:i])
+    stub.oracle.reset()
+    stub.calls.clear()
+    out = dec.generate_ids(prompt, 10, eos_token_id=ref[k], **kw)
+    assert out == ref[:k + 1]
+    assert dec.position == len(prompt) - 1 + k + 1
+    sampled = [c for c in stub.calls if c[0] == "generate_sampled"]
+    assert [c[2] for c in sampled] == list(range(4, 4 + k + 1, 3))  # chunk starts
+    assert all(c[1] == (5 if i == 0 else ref[3 * i - 1]) for i, c in enumerate(sampled))
+    # greedy settings take the greedy path
+    stub.calls.clear()
+    stub.oracle.reset()
+    dec.generate_ids(prompt, 4, temperature=0.7, top_k=1)
+    assert stub.calls[-1][0] == "generate_nosync"
+    with pytest.raises(ValueError):
+        dec.generate_sampled(1, 2, temperature=1.0, top_k=-3)
 
 
 def test_positions_past_the_cache_raise(qa_cpu):
