@@ -163,7 +163,8 @@ struct DeviceState {
   Workspace fixed;                // the `scratch` array of this device (no allocation)
   LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
   char* pf = nullptr;             // prefill activations (PF_BYTES), on first use
-  char* smp = nullptr;            // sampled generation: one step's logits and token (SMP_BYTES)
+  char* smp = nullptr;            // sampler work area, sampled generation's step buffers (SMP_BYTES)
+  u32 smp_parity = 0;             // sampler launches so far (selects the work area copy)
   u64 clk_khz = 100000;
   u64 deadline = 0;
   u64* trace = nullptr;
@@ -322,9 +323,11 @@ constexpr long PF_BAR_BYTES = 4096;  // barrier counters and flags, one 128-byte
 constexpr long PF_TS = PF_BAR + PF_BAR_BYTES;
 constexpr long PF_BYTES = PF_TS + 8L * ((PF_NTS + 31) / 32 * 32);
 
-// sampled generation: one step's fp32 logits, the step's greedy id (unused), the sampled id, and
-// the embedding row of the sampled id (the next decode step's one-row embedding table)
-constexpr long SMP_LOGITS = 0;
+// sampler buffer: the sampler's work area, one step's fp32 logits, the step's greedy id (unused),
+// the sampled id, and the embedding row of the sampled id (the next decode step's one-row
+// embedding table)
+constexpr long SMP_WORK = 0;
+constexpr long SMP_LOGITS = SMP_WORK + (smp::WORK_BYTES + 255) / 256 * 256;
 constexpr long SMP_ARGMAX = SMP_LOGITS + (long)VOCAB * 4;
 constexpr long SMP_TOKEN = SMP_ARGMAX + 256;
 constexpr long SMP_ROW = SMP_TOKEN + 256;
@@ -337,9 +340,32 @@ bool sample_args_ok(float temperature, int top_k, float top_p) {
   return temperature == temperature && top_k >= 0 && top_p == top_p;
 }
 
-int launch_sampler(const smp::SParams& S, hipStream_t stream) {
-  hipLaunchKernelGGL(smp::qwen_sample_kernel, dim3(1), dim3(smp::NT), 0, stream, S);
-  return hipGetLastError() == hipSuccess ? QWEN_OK : QWEN_ERR_LAUNCH;
+// the device's sampler buffer (allocated and cleared on first use); caller holds g_mu
+int sampler_buffer(DeviceState* st, hipStream_t stream) {
+  if (st->smp) return QWEN_OK;
+  int rc = heap_workspace(st);  // the status word the sampler reports to
+  if (rc != QWEN_OK) return rc;
+  void* p = nullptr;
+  if (hipMalloc(&p, SMP_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+  if (zero_words(p, SMP_BYTES, stream) != QWEN_OK) {
+    (void)hipFree(p);
+    return QWEN_ERR_LAUNCH;
+  }
+  st->smp = (char*)p;
+  return QWEN_OK;
+}
+
+// one sampler launch on the device's work area; caller holds g_mu
+int launch_sampler(DeviceState* st, smp::SParams& S, hipStream_t stream) {
+  S.work = (u64*)(st->smp + SMP_WORK);
+  S.parity = st->smp_parity++;
+  S.status = st->heap.status;
+  S.deadline = st->deadline;
+  void* args[] = {&S};
+  if (hipLaunchCooperativeKernel((const void*)smp::qwen_sample_kernel, dim3(smp::NB), dim3(smp::NT), args, 0,
+                                 stream) != hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  return QWEN_OK;
 }
 
 int fill_decode(KParams& P, const void* embed, const LDGLayerWeight* lw, const void* fnorm, const void* lm_head,
@@ -559,7 +585,12 @@ extern "C" int qwen_prefill_timestamps(unsigned long long* out, int max_entries)
 
 extern "C" int qwen_sample(const float* logits, int n, float temperature, int top_k, float top_p,
                            unsigned long long seed, unsigned int step, int* out_token, hipStream_t stream) {
-  if (!logits || !out_token || n < 1 || !sample_args_ok(temperature, top_k, top_p)) return QWEN_ERR_ARG;
+  if (!logits || !out_token || n < 1 || n > smp::MAX_N || !sample_args_ok(temperature, top_k, top_p))
+    return QWEN_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceState* st = nullptr;
+  int rc = device_state(&st);
+  if (rc != QWEN_OK || (rc = sampler_buffer(st, stream)) != QWEN_OK) return rc;
   smp::SParams S;
   memset(&S, 0, sizeof(S));
   S.logits = logits;
@@ -571,7 +602,7 @@ extern "C" int qwen_sample(const float* logits, int n, float temperature, int to
   S.step = step;
   S.out_token = out_token;
   S.eos = -1;
-  return launch_sampler(S, stream);
+  return launch_sampler(st, S, stream);
 }
 
 extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
@@ -591,15 +622,10 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
       !sample_args_ok(temperature, top_k, top_p))
     return QWEN_ERR_ARG;
   char* buf = nullptr;
+  DeviceState* st = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_mu);
-    DeviceState* st = nullptr;
-    if ((rc = device_state(&st)) != QWEN_OK) return rc;
-    if (!st->smp) {
-      void* p = nullptr;
-      if (hipMalloc(&p, SMP_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-      st->smp = (char*)p;
-    }
+    if ((rc = device_state(&st)) != QWEN_OK || (rc = sampler_buffer(st, stream)) != QWEN_OK) return rc;
     buf = st->smp;
   }
   float* logits = (float*)(buf + SMP_LOGITS);
@@ -633,7 +659,8 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
     S.step = (u32)(start_position + s);
     S.out_log = output_log + s;
     S.index = s;
-    if ((rc = launch_sampler(S, stream)) != QWEN_OK) return rc;
+    std::lock_guard<std::mutex> lock(g_mu);
+    if ((rc = launch_sampler(st, S, stream)) != QWEN_OK) return rc;
   }
   return QWEN_OK;
 }
@@ -722,6 +749,10 @@ extern "C" int qwen_last_error(void) {
   if (hipDeviceSynchronize() != hipSuccess) return QWEN_ERR_LAUNCH;
   const int a = take_status(st.heap);
   const int b = take_status(st.fixed);
+  // a failed sampler launch can leave its work area (histograms, barrier words) dirty
+  if (a != QWEN_OK && st.smp &&
+      (zero_words(st.smp + SMP_WORK, smp::WORK_BYTES / 8 * 8, nullptr) != QWEN_OK || hipDeviceSynchronize() != hipSuccess))
+    return QWEN_ERR_LAUNCH;
   return a != QWEN_OK ? a : b;
 }
 
