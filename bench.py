@@ -219,23 +219,27 @@ def trace_breakdown(tr, layers=28):
     """Per-stage times of one traced token (tr: [256 workgroups, 8 * layers + 1, events] of
     100 MHz ticks; event 0 = starts waiting, 1 = has its input, 3 = stored and acknowledged),
     means over layers 1 .. layers - 1: 'hop' from the previous stage's last store to this
-    stage's last input, 'proc' from the last input to the last store, and the grouping
-    GEMV (qkv, o_proj, gate_up, down) / attention (attention, combine) / residual sums."""
+    stage's last input, 'proc' from the last input to the last store, 'stage' their sum (the
+    stage's share of the critical path), 'median_wg' the same end point for the median
+    workgroup instead of the last (the difference is what the slowest workgroup costs), and
+    the grouping GEMV (qkv, o_proj, gate_up, down) / attention (attention, combine) / residual
+    sums."""
     import numpy as np
 
     t = (tr.astype(np.int64) - tr[:, 0, 0].min()) / 100.0
-    lines = ["stage       hop_us  proc_us  stage_us"]
+    lines = ["stage       hop_us  proc_us  stage_us  median_wg_us"]
     per = {}
     for st, name in enumerate(STAGES):
-        hop, proc, dur = [], [], []
+        hop, proc, dur, med = [], [], [], []
         for layer in range(1, layers):
             s = 8 * layer + st
             last_prev = t[:, s - 1, 3].max()
             hop.append(t[:, s, 1].max() - last_prev)
             proc.append(t[:, s, 3].max() - t[:, s, 1].max())
             dur.append(t[:, s, 3].max() - last_prev)
+            med.append(np.median(t[:, s, 3]) - last_prev)  # the median workgroup's store
         per[name] = float(np.mean(dur))
-        lines.append(f"{name:10s} {np.mean(hop):7.2f} {np.mean(proc):8.2f} {np.mean(dur):9.2f}")
+        lines.append(f"{name:10s} {np.mean(hop):7.2f} {np.mean(proc):8.2f} {np.mean(dur):9.2f} {np.mean(med):13.2f}")
     layer = np.mean([t[:, 8 * l + 7, 3].max() - t[:, 8 * l - 1, 3].max() for l in range(1, layers)])
     lm = t[:, 8 * layers, 3].max() - t[:, 8 * layers - 1, 3].max()
     token = t[:, 8 * layers, 3].max()

@@ -155,7 +155,8 @@ def load_weights(model_name="Qwen/Qwen3-0.6B", verbose: bool = True):
     ``model_name`` must be a directory holding ``*.safetensors`` (and, for text
     generation, the tokenizer files). Tensors are cast to fp16 on the GPU and
     returned in the reference's dictionary layout (reference lines 97-174):
-    11 per-layer tensors in ``LDGLayerWeight`` order, tied lm_head.
+    11 per-layer tensors in ``LDGLayerWeight`` order; the lm_head is the
+    embedding (tied, as Qwen3-0.6B) unless the checkpoint has ``lm_head.weight``.
     """
     if not os.path.isdir(model_name):
         raise RuntimeError(
@@ -187,7 +188,7 @@ def load_weights(model_name="Qwen/Qwen3-0.6B", verbose: bool = True):
         embed_weight=embed_weight,
         layer_weights=layer_weights,
         final_norm_weight=dev("model.norm.weight"),
-        lm_head_weight=embed_weight,  # tied embeddings
+        lm_head_weight=dev("lm_head.weight") if "lm_head.weight" in state else embed_weight,
         cos_table=cos_table,
         sin_table=sin_table,
     )

@@ -625,3 +625,49 @@ def test_argument_errors_raise(ext, full, qa):
                             run.norm_out, run.norm_out, run.hidden, run.hidden, run.hidden, run.hidden,
                             run.norm_out, run.norm_out, run.norm_out, 28, 0, MAX_SEQ, SCALE)
     assert ext.last_error() == 0
+
+
+def test_checkpoint_directory_feeds_the_engine(ext, qa, tmp_path):
+    """load_weights on a local checkpoint directory as a real one holds it: HF tensor names,
+    bf16, non-unit norms distinct per layer and field, its own lm_head.weight. The engine's
+    tensors must equal the bf16 values cast to fp16 bit for bit, and the engine on them must
+    match the oracle on the same values (teacher-forced, 12 steps: tokens except near-ties,
+    logits, hidden)."""
+    from safetensors.torch import save_file
+
+    hw = qw.host_weights(seed=7, std=0.02, norms="random", untied=True)
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16)
+    state = {"model.embed_tokens.weight": bf(hw.embed), "model.norm.weight": bf(hw.final_norm),
+             "lm_head.weight": bf(hw.lm_head)}
+    for i, layer in enumerate(hw.layers):
+        for key, t in zip(qa._LAYER_KEYS, layer):
+            state[f"model.layers.{i}.{key}"] = bf(t)
+    save_file(state, str(tmp_path / "model.safetensors"))
+    # what the engine must receive: the checkpoint's bf16 values as fp16
+    h16 = lambda t: t.to(torch.float16).numpy()
+    ref = qw.HostWeights(shape=hw.shape, embed=h16(state["model.embed_tokens.weight"]),
+                         layers=[[h16(state[f"model.layers.{i}.{k}"]) for k in qa._LAYER_KEYS]
+                                 for i in range(len(hw.layers))],
+                         final_norm=h16(state["model.norm.weight"]), cos=hw.cos, sin=hw.sin,
+                         lm_head=h16(state["lm_head.weight"]))
+    del state
+    w, _ = qa.load_weights(str(tmp_path), verbose=False)
+    assert w["lm_head_weight"].data_ptr() != w["embed_weight"].data_ptr()
+    assert np.array_equal(w["embed_weight"].cpu().numpy().view(np.uint16), ref.embed.view(np.uint16))
+    assert np.array_equal(w["lm_head_weight"].cpu().numpy().view(np.uint16), ref.lm_head.view(np.uint16))
+    assert np.array_equal(w["final_norm_weight"].cpu().numpy().view(np.uint16), ref.final_norm.view(np.uint16))
+    for i in (0, 13, 27):
+        for f in range(11):
+            got = w["layer_weights"][11 * i + f].cpu().numpy().view(np.uint16)
+            assert np.array_equal(got, ref.layers[i][f].view(np.uint16)), (i, f)
+    assert torch.equal(w["cos_table"].cpu(), torch.from_numpy(hw.cos))
+    packed = qa._pack_layer_weights(w["layer_weights"])
+    ids = qw.synthetic_prompt(12, seed=21)
+    toks, logits, hidden = Run(w, packed, 28).forced(ext, ids, 0)
+    o = orc.Oracle(ref)
+    steps = []
+    for p, t in enumerate(ids):
+        st = o.step(t, p)
+        st["gap"] = orc.top2_gap(st["logits"])
+        steps.append(st)
+    _compare_steps(steps, toks, logits, hidden, 0, "checkpoint directory")
