@@ -129,6 +129,11 @@ __global__ void __launch_bounds__(BLOCK, 1) qwen_placement_probe(u32* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
+// the prefill kernel's geometry (two 256-thread workgroups per CU): each records its XCC
+__global__ void __launch_bounds__(pf::NT, pf::WG_PER_CU) qwen_placement_probe_pf(u32* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
 // zeroes n 8-byte words (a kernel, not hipMemsetAsync: callers may capture the stream)
 __global__ void qwen_zero_words(u64* p, long n) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
@@ -198,18 +203,21 @@ int zero_words(void* p, long bytes, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? QWEN_OK : QWEN_ERR_LAUNCH;
 }
 
-// Every workgroup w of a 256 x 512 launch must run on XCD w % 8: the work partition and the
-// XCD-local exchange stores rely on it. Checked once per device with a probe launch that
-// writes into `buf` (NWG words).
-int check_placement(u32* buf, hipStream_t s) {
+// Every workgroup w of the decode launch (256 x 512) and of the prefill launch (512 x 256) must
+// run on XCD w % 8: the decode's work partition and XCD-local exchange stores, and the prefill's
+// per-XCD barrier (one L2 write-back and invalidate per XCD) rely on it. Checked once per device
+// and geometry with a probe launch that writes into `buf` (n words).
+int check_placement(const void* probe, int n, int threads, u32* buf, hipStream_t s) {
   void* args[] = {&buf};
-  if (hipLaunchCooperativeKernel((const void*)qwen_placement_probe, dim3(NWG), dim3(BLOCK), args, 0, s) != hipSuccess)
+  if (hipLaunchCooperativeKernel(probe, dim3(n), dim3(threads), args, 0, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
     return QWEN_ERR_LAUNCH;
-  u32 xcc[NWG];
-  if (hipMemcpy(xcc, buf, sizeof(xcc), hipMemcpyDeviceToHost) != hipSuccess) return QWEN_ERR_LAUNCH;
-  for (int w = 0; w < NWG; ++w)
+  static u32 xcc[2 * NWG];
+  if (n > 2 * NWG || hipMemcpy(xcc, buf, sizeof(u32) * n, hipMemcpyDeviceToHost) != hipSuccess)
+    return QWEN_ERR_LAUNCH;
+  for (int w = 0; w < n; ++w)
     if ((int)(xcc[w] & 15) != xcd_of(w)) {
-      fprintf(stderr, "qwen_megakernel: workgroup %d runs on XCC %u, the work partition needs XCC %d\n", w,
+      fprintf(stderr, "qwen_megakernel: workgroup %d of %d runs on XCC %u, the kernel needs XCC %d\n", w, n,
               xcc[w] & 15, xcd_of(w));
       return QWEN_ERR_DEVICE;
     }
@@ -249,7 +257,7 @@ int device_state(DeviceState** out) {
       st.err = QWEN_ERR_LAUNCH;
       return st.err;
     }
-    st.err = check_placement((u32*)fixed, nullptr);
+    st.err = check_placement((const void*)qwen_placement_probe, NWG, BLOCK, (u32*)fixed, nullptr);
     if (st.err != QWEN_OK) return st.err;
     if (zero_words(fixed, WORKSPACE_BYTES, nullptr) != QWEN_OK || hipDeviceSynchronize() != hipSuccess) {
       st.err = QWEN_ERR_LAUNCH;
@@ -529,10 +537,14 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   if (!st->pf) {
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)pf::qwen_prefill_kernel, pf::NT, 0) !=
-            hipSuccess || occ < 1)
+            hipSuccess || occ < pf::WG_PER_CU)
       return QWEN_ERR_DEVICE;
     void* p = nullptr;
     if (hipMalloc(&p, PF_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
+    if ((rc = check_placement((const void*)qwen_placement_probe_pf, pf::NWG_PF, pf::NT, (u32*)p, stream)) != QWEN_OK) {
+      (void)hipFree(p);
+      return rc;
+    }
     st->pf = (char*)p;
   }
   pf::PParams P;
@@ -560,7 +572,7 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.attn_scale = attn_scale;
   if (zero_words(P.bar, PF_BAR_BYTES, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
   void* args[] = {&P};
-  if (hipLaunchCooperativeKernel((const void*)pf::qwen_prefill_kernel, dim3(NWG), dim3(pf::NT), args, 0, stream) !=
+  if (hipLaunchCooperativeKernel((const void*)pf::qwen_prefill_kernel, dim3(pf::NWG_PF), dim3(pf::NT), args, 0, stream) !=
       hipSuccess)
     return QWEN_ERR_LAUNCH;
   return QWEN_OK;
