@@ -328,7 +328,8 @@ def run_generate_e2e(args):
     dec = qa.Decoder(weights=w, verbose=False)
     n_prompt, n_new = 1000, 1000
     prompt = qw.synthetic_prompt(n_prompt, seed=1)
-    sampling = dict(temperature=0.8, top_k=50, top_p=0.95, seed=7) if args.workload == "sampled" else {}
+    sampling = {"sampled": dict(temperature=0.8, top_k=50, top_p=0.95, seed=7),
+                "sampled_t": dict(temperature=0.8, seed=7)}.get(args.workload, {})
     ts = []
     for rep in range(args.warmup + args.steps):
         torch.cuda.synchronize()
@@ -342,11 +343,13 @@ def run_generate_e2e(args):
     cfg = {"prompt": n_prompt, "new_tokens": n_new, "positions": f"0..{n_prompt + n_new - 2}"}
     if sampling:
         cfg.update(sampling)
-        return aux_line("Decoder.generate tokens/sec with sampling (temperature 0.8, top-k 50, top-p 0.95), "
-                        "1000-id prompt + 1000 new tokens, prefill included", round(n_new / ms * 1e3, 2),
-                        "tokens/s", True, "sampled", cfg,
-                        "fast::qwen_decode_kernel + smp::qwen_sample_kernel + pf::qwen_prefill_kernel",
-                        algorithmic_bytes(n_prompt - 1, n_new), ms, args.steps, args.warmup)
+        what = ("temperature 0.8, top-k 50, top-p 0.95" if "top_k" in sampling else "temperature 0.8")
+        kernels = ("fast::qwen_decode_kernel + smp::qwen_sample_kernel" if "top_k" in sampling
+                   else "sampled::qwen_decode_kernel")
+        return aux_line(f"Decoder.generate tokens/sec with sampling ({what}), 1000-id prompt + 1000 new tokens, "
+                        "prefill included", round(n_new / ms * 1e3, 2), "tokens/s", True, args.workload, cfg,
+                        kernels + " + pf::qwen_prefill_kernel", algorithmic_bytes(n_prompt - 1, n_new), ms,
+                        args.steps, args.warmup)
     return aux_line("Decoder.generate tokens/sec, 1000-id prompt + 1000 new tokens, prefill included",
                     round(n_new / ms * 1e3, 2), "tokens/s", True, "generate", cfg,
                     "fast::qwen_decode_kernel + pf::qwen_prefill_kernel",
@@ -366,11 +369,12 @@ def main():
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
                          "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, events], 100 MHz ticks)")
     ap.add_argument("--workload", default="c4",
-                    choices=["c4", "c3", "c0", "c1", "c2", "prefill", "generate", "sampled"],
+                    choices=["c4", "c3", "c0", "c1", "c2", "prefill", "generate", "sampled", "sampled_t"],
                     help="c4 (default): the headline decode at context 1921..2048; c3: 128-id prompt + "
                          "generate_nosync 512; c0: 16 + 32; c1: isolated lm_head + argmax; c2: isolated MLP block; "
                          "prefill: batched prefill of 1920 ids; generate: Decoder.generate_ids 1000 + 1000 "
-                         "with its prefill; sampled: the same with temperature 0.8, top-k 50, top-p 0.95")
+                         "with its prefill; sampled: the same with temperature 0.8, top-k 50, top-p 0.95; "
+                         "sampled_t: with temperature 0.8 alone")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine runs one sequence on one MI355X; --gpus {args.gpus} "
@@ -381,7 +385,7 @@ def main():
         runs = {"c3": lambda: run_generate(args, 128, 512, "c3"), "c0": lambda: run_generate(args, 16, 32, "c0"),
                 "c1": lambda: run_lm_head(args), "c2": lambda: run_mlp(args),
                 "prefill": lambda: run_prefill(args), "generate": lambda: run_generate_e2e(args),
-                "sampled": lambda: run_generate_e2e(args)}
+                "sampled": lambda: run_generate_e2e(args), "sampled_t": lambda: run_generate_e2e(args)}
         print(json.dumps(runs[args.workload]()), flush=True)
         return
 

@@ -195,16 +195,19 @@ int qwen_sample(const float* logits, int n, float temperature, int top_k, float 
 
 /* Sampled generation (no counterpart in the reference): generate_nosync whose
  * every next token comes from qwen_sample over that step's logits (seed,
- * step = the position of the step's input token) instead of the argmax. Runs
- * as num_steps pairs of launches (a decode step, then the sampler) with no
- * host synchronisation. With eos_token_id >= 0 the generation ends after the
+ * step = the position of the step's input token) instead of the argmax. With
+ * temperature alone (top_k 0 and top_p >= 1) the decode kernel's sampling build
+ * draws each token itself in one launch of num_steps steps; otherwise it runs
+ * as num_steps pairs of launches (a decode step, then the sampler); neither
+ * synchronises with the host. With eos_token_id >= 0 the generation ends after the
  * first sampled eos: output_log[0 .. n) holds the sampled ids, eos last when it
  * was reached, later entries are -1, and n = *out_count (device int32,
  * nullable) <= num_steps; the K/V cache holds positions start_position ..
- * start_position + n - 1. The launches after the eos still run (the host
- * enqueued them) and their results mean nothing: K/V entries past that
- * range, hidden_buffer and g_normalized; a caller that expects an early eos
- * enqueues shorter runs. Allocates a 610 KB per-device buffer on first use. */
+ * start_position + n - 1. In the pairs-of-launches form the launches after
+ * the eos still run (the host enqueued them) and their results mean nothing:
+ * K/V entries past that range, hidden_buffer and g_normalized; a caller that
+ * expects an early eos enqueues shorter runs. That form allocates a 759 KB
+ * per-device buffer on first use. */
 int qwen_generate_sampled(
     int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
     const LDGLayerWeight* layer_weights, const void* final_norm_weight,

@@ -11,8 +11,8 @@ from the softmax), with two choices fixed where they leave freedom:
 
 * ties at a top-k or top-p boundary are all kept (HuggingFace keeps top-k ties
   too; its top-p boundary among equal logits depends on its sort order);
-* the draw is a Gumbel-max pick, ``argmax_j (l_j - M) / T + g_j`` over the
-  kept tokens, with ``g_j = -log(-log(u_j))`` and ``u_j`` from Philox4x32-10
+* the draw is a Gumbel-max pick, ``argmax_j l_j / T + g_j`` over the kept
+  tokens, with ``g_j = -log(-log(u_j))`` and ``u_j`` from Philox4x32-10
   (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as easy as 1, 2, 3",
   SC'11) of counter ``(j, step, 0, 0)`` under key ``(seed & 0xffffffff,
   seed >> 32)``: ``u = ((x0 >> 9) + 0.5) / 2^23``, exact in fp32 and inside
@@ -148,7 +148,7 @@ def sample(logits: np.ndarray, temperature: float, top_k: int = 0, top_p: float 
         return (greedy, {"gap": math.inf, "greedy": True}) if details else greedy
     mask, info = kept_set(x, temperature, top_k, top_p)
     with np.errstate(invalid="ignore"):
-        score = (x - m) / np.float32(temperature) + gumbel(seed, step, x.size)
+        score = x / np.float32(temperature) + gumbel(seed, step, x.size)
     score = np.where(mask, score, np.float32(-np.inf)).astype(np.float32)
     tok = argmax_lowest(np.where(mask, score, np.float32(np.nan)))
     if not details:

@@ -384,7 +384,9 @@ class Decoder:
             raise ValueError(f"invalid sampling parameters temperature={temperature} top_k={top_k} top_p={top_p}")
         gen = _require_megakernel_op("generate_sampled")
         eos = -1 if eos_token_id is None else int(eos_token_id)
-        chunk = max_tokens if eos < 0 else SAMPLED_CHUNK
+        # temperature alone runs as one launch that checks eos on the device: no chunking
+        one_launch = top_k == 0 and top_p >= 1.0
+        chunk = max_tokens if eos < 0 or one_launch else SAMPLED_CHUNK
         out, first = [], int(first_token_id)
         while len(out) < max_tokens:
             m = min(chunk, max_tokens - len(out))

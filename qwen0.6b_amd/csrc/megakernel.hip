@@ -103,20 +103,60 @@ struct KParams {
   int mode, num_layers, first_token, start_pos, num_steps, max_seq;
   float attn_scale;
   u32 epoch0;
+  // the sampling build of the kernel: every next token is the argmax of logit / temperature +
+  // Gumbel noise (seed, position) instead of the logit's (temperature sampling, on the device)
+  float temperature;
+  u64 seed;
+  int sample;              // host side: launch the sampling build
 };
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds of two 32x32 -> 64 multiplies
+// with the published multipliers and key increments; returns the first output word
+__device__ __forceinline__ u32 philox_x0(u32 c0, u32 c1, u32 c2, u32 c3, u32 k0, u32 k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const u64 p0 = (u64)0xD2511F53u * c0, p1 = (u64)0xCD9E8D57u * c2;
+    const u32 n0 = (u32)(p1 >> 32) ^ c1 ^ k0, n2 = (u32)(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = (u32)p1;
+    c2 = n2;
+    c3 = (u32)p0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+
+// Gumbel(0, 1) noise of token j at `step` (the position of the step's input token) under `seed`:
+// g = -log(-log(u)) with u = (top 23 bits of Philox of counter (j, step, 0, 0), key (seed low,
+// seed high), + 0.5) / 2^23, every step exact in fp32, so u lies in [2^-24, 1 - 2^-24] (24 bits
+// would round the largest value up to 1.0 and give g = +inf)
+__device__ __forceinline__ float gumbel(u64 seed, u32 step, u32 j) {
+  const u32 x = philox_x0(j, step, 0u, 0u, (u32)seed, (u32)(seed >> 32));
+  const float u = ((float)(x >> 9) + 0.5f) * (1.0f / 8388608.0f);
+  return -logf(-logf(u));
+}
 
 // ------------------------------------------------------------------------------------
 // device code: the production kernel, and a copy that records per-stage timestamps
 
 namespace fast {
 constexpr bool kTrace = false;
+constexpr bool kSample = false;
 #include "decode_body.inc"
 }  // namespace fast
 
 namespace traced {
 constexpr bool kTrace = true;
+constexpr bool kSample = false;
 #include "decode_body.inc"
 }  // namespace traced
+
+namespace sampled {
+constexpr bool kTrace = false;
+constexpr bool kSample = true;
+#include "decode_body.inc"
+}  // namespace sampled
 
 // the batched prefill kernel (namespace pf)
 #include "prefill_body.inc"
@@ -313,7 +353,9 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
   }
   w.epoch = (u32)next;
   void* args[] = {&P};
-  const void* kernel = P.trace ? (const void*)traced::qwen_decode_kernel : (const void*)fast::qwen_decode_kernel;
+  const void* kernel = P.trace    ? (const void*)traced::qwen_decode_kernel
+                       : P.sample ? (const void*)sampled::qwen_decode_kernel
+                                  : (const void*)fast::qwen_decode_kernel;
   if (hipLaunchCooperativeKernel(kernel, dim3(NWG), dim3(BLOCK), args, 0, stream) != hipSuccess)
     return QWEN_ERR_LAUNCH;
   return QWEN_OK;
@@ -633,6 +675,18 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
   if (!output_log || first_token_id < 0 || first_token_id >= VOCAB || eos_token_id < -1 || eos_token_id >= VOCAB ||
       !sample_args_ok(temperature, top_k, top_p))
     return QWEN_ERR_ARG;
+  if (temperature > 0.f && (top_k == 0 || top_k >= VOCAB) && !(top_p < 1.f)) {
+    // temperature alone: the decode kernel's sampling build draws every token itself (one
+    // launch, eos checked on the device as in qwen_generate_until)
+    P.first_token = first_token_id;
+    P.out_tokens = output_log;
+    P.out_count = out_count;
+    P.eos = eos_token_id;
+    P.temperature = temperature;
+    P.seed = seed;
+    P.sample = 1;
+    return launch(P, stream);
+  }
   char* buf = nullptr;
   DeviceState* st = nullptr;
   {
