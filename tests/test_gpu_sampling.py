@@ -251,3 +251,55 @@ def test_decoder_sampling_api(qa, full):
         assert c == a[:5] and dec.position == len(PROMPT) - 1 + 5
     with pytest.raises(ValueError):
         dec.generate_sampled(1, 4, temperature=1.0, top_k=-1)
+
+
+def _lib():
+    import ctypes
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "qwen0.6b_amd",
+                        "libqwen_megakernel.so")
+    return ctypes.CDLL(path)
+
+
+def test_sampling_c_abi(ext, full):
+    """qwen_sample and qwen_generate_sampled through the C-ABI (ctypes, torch's current stream):
+    the same ids as the pybind ops; argument errors come back as QWEN_ERR_ARG (1)."""
+    import ctypes
+
+    lib = _lib()
+    vp, i32, f32, u64, u32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_ulonglong, ctypes.c_uint
+    lib.qwen_sample.argtypes = [vp, i32, f32, i32, f32, u64, u32, vp, vp]
+    lib.qwen_sample.restype = i32
+    lib.qwen_generate_sampled.argtypes = [i32, i32, i32] + [vp] * 12 + [i32, i32, i32, f32, f32, i32, f32, u64, vp]
+    lib.qwen_generate_sampled.restype = i32
+    stream = torch.cuda.current_stream().cuda_stream
+    x = torch.from_numpy(_logits("normal", V, np.random.default_rng(9))).cuda()
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for args in [(0.7, 50, 0.9, 5, 77), (1.0, 0, 1.0, 6, 78), (0.0, 0, 1.0, 0, 0)]:
+        t_, k_, p_, seed, step = args
+        assert lib.qwen_sample(x.data_ptr(), V, t_, k_, p_, seed, step, out.data_ptr(), stream) == 0
+        torch.cuda.synchronize()
+        assert int(out.item()) == int(ext.sample(x, t_, k_, p_, seed, step).item())
+    assert lib.qwen_sample(x.data_ptr(), 0, 1.0, 0, 1.0, 0, 0, out.data_ptr(), stream) == 1      # n < 1
+    assert lib.qwen_sample(x.data_ptr(), V, float("nan"), 0, 1.0, 0, 0, out.data_ptr(), stream) == 1
+    assert lib.qwen_sample(x.data_ptr(), V, 1.0, -1, 1.0, 0, 0, out.data_ptr(), stream) == 1     # top_k < 0
+    assert lib.qwen_sample(None, V, 1.0, 0, 1.0, 0, 0, out.data_ptr(), stream) == 1
+    start, n = len(PROMPT) - 1, 12
+    for t_, k_, p_ in [(0.9, 0, 1.0), (0.9, 40, 0.9)]:
+        a = _prefilled(full, ext)
+        ref, _ = a.sampled(ext, PROMPT[-1], n, start, t_, k_, p_, 123)
+        b = _prefilled(full, ext)
+        ids = torch.full((n,), -7, dtype=torch.int32, device="cuda")
+        cnt = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ts = [t.data_ptr() for t in b.tensors()]
+        rc = lib.qwen_generate_sampled(PROMPT[-1], n, -1, ts[0], ts[1], ts[2], ts[3], ts[4], ts[5], ts[6], ts[7],
+                                       ts[8], ts[9], ids.data_ptr(), cnt.data_ptr(), 28, start, MAX_SEQ, SCALE, t_,
+                                       k_, p_, 123, stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert ext.last_error() == 0
+        assert ids.cpu().tolist() == ref and int(cnt.item()) == n
+    bad = lib.qwen_generate_sampled(PROMPT[-1], n, -2, *([None] * 12), 28, start, MAX_SEQ, SCALE, 1.0, 0, 1.0, 1,
+                                    stream)
+    assert bad == 1
