@@ -40,6 +40,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -362,16 +363,57 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
 }
 
 // prefill activations for up to MAX_SEQ_LIMIT positions: residual X fp32 [n, 1024], q and the
-// attention output fp16 [n, 2048] each, SiLU * up fp16 [n, 3072], then the barrier counter
+// attention output fp16 [n, 2048] each, SiLU * up fp16 [n, 3072], then the barrier counters and
+// the split attention items' arrival counters (zeroed before every launch), the timestamps and
+// the split items' partial results
 constexpr long PF_X = 0;
 constexpr long PF_Q = PF_X + (long)MAX_SEQ_LIMIT * HIDDEN * 4;
 constexpr long PF_AO = PF_Q + (long)MAX_SEQ_LIMIT * QSZ * 2;
 constexpr long PF_IM = PF_AO + (long)MAX_SEQ_LIMIT * QSZ * 2;
 constexpr long PF_BAR = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
 constexpr int PF_NTS = 1 + 1 + 5 * MAX_LAYERS;  // launch start, then every grid barrier
-constexpr long PF_BAR_BYTES = 4096;  // barrier counters and flags, one 128-byte line each
+constexpr long PF_BAR_LINES = 4096;              // barrier counters and flags, one 128-byte line each
+constexpr long PF_ACNT = PF_BAR + PF_BAR_LINES;
+constexpr long PF_BAR_BYTES = PF_BAR_LINES + 4L * pf::MAX_QB * NKV;
 constexpr long PF_TS = PF_BAR + PF_BAR_BYTES;
-constexpr long PF_BYTES = PF_TS + 8L * ((PF_NTS + 31) / 32 * 32);
+constexpr long PF_PART = (PF_TS + 8L * ((PF_NTS + 31) / 32 * 32) + 255) / 256 * 256;
+constexpr long PF_BYTES = PF_PART + 4L * pf::MAX_PSLOTS * NKV * pf::PART_FLOATS;
+static_assert(PF_BAR_BYTES % 4 == 0 && PF_PART % 256 == 0, "prefill workspace alignment");
+
+// The attention work of a prefill of n positions from position start: query block b (positions
+// start + 32 b ..) reads key blocks 0 .. nkb(b) - 1 (64 keys each, causal), in chunks of 8 key
+// blocks; a block with more than one chunk is split into units (the kernel merges their partial
+// results). Units are sorted longest first (ties: later query block first, then chunk order),
+// the order in which the kernel deals them out.
+static int prefill_units(int n, int start, pf::PParams& P) {
+  const int nqb = (n + pf::QR - 1) / pf::QR;
+  if (nqb > pf::MAX_QB) return QWEN_ERR_ARG;
+  struct U {
+    int cost, b, c, s;
+  } u[pf::MAX_UNITS];
+  int nu = 0, slot = 0;
+  for (int b = 0; b < nqb; ++b) {
+    const int qmax = (pf::QR * b + pf::QR < n ? pf::QR * b + pf::QR : n) - 1 + start;
+    const int nkb = qmax / pf::QB + 1;
+    const int sb = (nkb + pf::KCHUNK - 1) / pf::KCHUNK;
+    if (sb > pf::MAX_CHUNKS || nu + sb > pf::MAX_UNITS) return QWEN_ERR_ARG;
+    P.pslot[b] = (unsigned char)(sb > 1 ? slot : 0);
+    if (sb > 1) slot += sb;
+    for (int c = 0; c < sb; ++c) {
+      const int left = nkb - pf::KCHUNK * c;
+      u[nu++] = {left < pf::KCHUNK ? left : pf::KCHUNK, b, c, sb};
+    }
+  }
+  if (slot > pf::MAX_PSLOTS) return QWEN_ERR_ARG;
+  std::sort(u, u + nu, [](const U& x, const U& y) {
+    if (x.cost != y.cost) return x.cost > y.cost;
+    if (x.b != y.b) return x.b > y.b;
+    return x.c < y.c;
+  });
+  for (int i = 0; i < nu; ++i) P.unit[i] = (unsigned short)(u[i].b | u[i].c << 6 | (u[i].s - 1) << 8);
+  P.nunits = nu;
+  return QWEN_OK;
+}
 
 // sampler buffer: the sampler's work area, one step's fp32 logits, the step's greedy id (unused),
 // the sampled id, and the embedding row of the sampled id (the next decode step's one-row
@@ -604,7 +646,9 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.AO = (_Float16*)(st->pf + PF_AO);
   P.IM = (_Float16*)(st->pf + PF_IM);
   P.bar = (u32*)(st->pf + PF_BAR);
+  P.acnt = (u32*)(st->pf + PF_ACNT);
   P.ts = (u64*)(st->pf + PF_TS);
+  P.part = (float*)(st->pf + PF_PART);
   P.status = st->heap.status;
   P.deadline = st->deadline;
   P.n = n;
@@ -612,6 +656,7 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.num_layers = num_layers;
   P.max_seq = max_seq_len;
   P.attn_scale = attn_scale;
+  if ((rc = prefill_units(n, start_position, P)) != QWEN_OK) return rc;
   if (zero_words(P.bar, PF_BAR_BYTES, stream) != QWEN_OK) return QWEN_ERR_LAUNCH;
   void* args[] = {&P};
   if (hipLaunchCooperativeKernel((const void*)pf::qwen_prefill_kernel, dim3(pf::NWG_PF), dim3(pf::NT), args, 0, stream) !=

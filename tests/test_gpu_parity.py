@@ -257,17 +257,21 @@ def test_batched_prefill_matches_oracle(ext, rn, n):
         assert toks[0] == ref["tokens"][0]
 
 
-def test_batched_prefill_chunked_equals_whole(ext, full):
-    """Prefilling 200 ids as 77 + 123 (the second chunk at position 77, attending to the
-    first chunk's cache) gives the same K/V cache, bit for bit, as one prefill of all 200:
-    every position's arithmetic is the same in both, whatever tile or query block it lands
-    in."""
+@pytest.mark.parametrize("n,cuts", [(200, [77]), (1300, [77, 900])])
+def test_batched_prefill_chunked_equals_whole(ext, full, n, cuts):
+    """Prefilling n ids in pieces (each piece at its start position, attending to the
+    cache the earlier pieces wrote) gives the same K/V cache, bit for bit, as one prefill
+    of all n: every position's arithmetic is the same in both, whatever tile or query
+    block it lands in. At n = 1300 the later query blocks read up to 21 key blocks, so
+    their attention is split into key chunks (8 blocks each) in both runs, with query
+    blocks aligned differently in the pieces (starts 77 and 900)."""
     hw, w, packed = full
-    ids = qw.synthetic_prompt(200, seed=61)
+    ids = qw.synthetic_prompt(n, seed=61)
     a, b = Run(w, packed, 28), Run(w, packed, 28)
     _prefill(ext, a, ids, 0)
-    _prefill(ext, b, ids[:77], 0)
-    _prefill(ext, b, ids[77:], 77)
+    bounds = [0] + cuts + [n]
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        _prefill(ext, b, ids[lo:hi], lo)
     assert torch.equal(a.kc, b.kc) and torch.equal(a.vc, b.vc)
     assert torch.equal(a.hidden, b.hidden)
 
