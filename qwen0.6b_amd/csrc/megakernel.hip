@@ -363,14 +363,17 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
 }
 
 // prefill activations for up to MAX_SEQ_LIMIT positions: residual X fp32 [n, 1024], q and the
-// attention output fp16 [n, 2048] each, SiLU * up fp16 [n, 3072], then the barrier counters and
+// attention output fp16 [n, 2048] each, SiLU * up fp16 [n, 3072], the next RMSNorm's gained input
+// fp16 [n, 1024] and its block sums of squares fp32 [n, 32], then the barrier counters and
 // the split attention items' arrival counters (zeroed before every launch), the timestamps and
 // the split items' partial results
 constexpr long PF_X = 0;
 constexpr long PF_Q = PF_X + (long)MAX_SEQ_LIMIT * HIDDEN * 4;
 constexpr long PF_AO = PF_Q + (long)MAX_SEQ_LIMIT * QSZ * 2;
 constexpr long PF_IM = PF_AO + (long)MAX_SEQ_LIMIT * QSZ * 2;
-constexpr long PF_BAR = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
+constexpr long PF_XN = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
+constexpr long PF_SSQ = PF_XN + (long)MAX_SEQ_LIMIT * HIDDEN * 2;
+constexpr long PF_BAR = PF_SSQ + (long)MAX_SEQ_LIMIT * 32 * 4;
 constexpr int PF_NTS = 1 + 1 + 5 * MAX_LAYERS;  // launch start, then every grid barrier
 constexpr long PF_BAR_LINES = 4096;              // barrier counters and flags, one 128-byte line each
 constexpr long PF_ACNT = PF_BAR + PF_BAR_LINES;
@@ -645,6 +648,8 @@ extern "C" int qwen_prefill(const int* ids, int n, const void* embed_weight, con
   P.Q = (_Float16*)(st->pf + PF_Q);
   P.AO = (_Float16*)(st->pf + PF_AO);
   P.IM = (_Float16*)(st->pf + PF_IM);
+  P.XN = (_Float16*)(st->pf + PF_XN);
+  P.SSQ = (float*)(st->pf + PF_SSQ);
   P.bar = (u32*)(st->pf + PF_BAR);
   P.acnt = (u32*)(st->pf + PF_ACNT);
   P.ts = (u64*)(st->pf + PF_TS);
