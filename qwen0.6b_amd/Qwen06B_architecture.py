@@ -24,6 +24,7 @@ Differences from the reference, all additive:
 import math
 import os
 
+import numpy as np
 import torch
 
 try:
@@ -323,7 +324,8 @@ class Decoder:
             return
         if self._position + len(ids) > MAX_SEQ_LEN:
             raise RuntimeError(f"prefill of {len(ids)} ids at position {self._position} exceeds {MAX_SEQ_LEN}")
-        t = torch.tensor(ids, dtype=torch.int32, device=DEVICE)
+        # through numpy: half the host time of torch.tensor on a long Python list
+        t = torch.from_numpy(np.fromiter(ids, dtype=np.int32, count=len(ids))).to(DEVICE)
         qwen_megakernel_C.prefill(t, self._embed_weight, self._layer_weights_packed, self._cos_table,
                                   self._sin_table, self._k_cache, self._v_cache, self._hidden, self._num_layers,
                                   self._position, MAX_SEQ_LEN, self._attn_scale)
