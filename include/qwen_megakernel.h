@@ -162,8 +162,10 @@ int qwen_generate_nosync_noalloc(
  * writes the K/V cache of every one of those positions and, to hidden_buffer,
  * the last position's final-layer residual. No lm_head: the greedy token after
  * a prompt comes from a decode step of its last id. Ids outside [0, 151936)
- * are reported by qwen_last_error() (QWEN_ERR_BAD_TOKEN). Allocates a 36 MB
- * activation workspace per device on first use. */
+ * are reported by qwen_last_error() (QWEN_ERR_BAD_TOKEN). A prompt prefilled
+ * in pieces (each at its own start position) leaves the same K/V cache, bit for
+ * bit, as one call with all of it. Allocates a 109 MB workspace per device on
+ * first use (activations of up to 2048 positions, partial attention results). */
 int qwen_prefill(
     const int* ids, int n, const void* embed_weight,
     const LDGLayerWeight* layer_weights, const void* cos_table,
