@@ -257,14 +257,15 @@ def test_batched_prefill_matches_oracle(ext, rn, n):
         assert toks[0] == ref["tokens"][0]
 
 
-@pytest.mark.parametrize("n,cuts", [(200, [77]), (1300, [77, 900])])
+@pytest.mark.parametrize("n,cuts", [(200, [77]), (1300, [77, 900]), (2047, [1500, 2040])])
 def test_batched_prefill_chunked_equals_whole(ext, full, n, cuts):
     """Prefilling n ids in pieces (each piece at its start position, attending to the
     cache the earlier pieces wrote) gives the same K/V cache, bit for bit, as one prefill
     of all n: every position's arithmetic is the same in both, whatever tile or query
     block it lands in. At n = 1300 the later query blocks read up to 21 key blocks, so
     their attention is split into key chunks (8 blocks each) in both runs, with query
-    blocks aligned differently in the pieces (starts 77 and 900)."""
+    blocks aligned differently in the pieces (starts 77 and 900). At n = 2047 the last piece is
+    7 ids at position 2040, whose keys split into four chunks."""
     hw, w, packed = full
     ids = qw.synthetic_prompt(n, seed=61)
     a, b = Run(w, packed, 28), Run(w, packed, 28)
