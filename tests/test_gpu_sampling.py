@@ -69,6 +69,8 @@ def _logits(kind, n, rng):
         idx = rng.choice(n, max(2, n // 16), replace=False)
         x[idx[: len(idx) // 2]] = np.nan
         x[idx[len(idx) // 2:]] = -np.inf
+    elif kind == "ties":  # ~7000 tokens tied at the top value: a top-k boundary tie wider than any
+        x = np.round(rng.standard_normal(n) * 0.3).astype(np.float32)  # workgroup's candidate list
     elif kind == "peaked":  # one dominant token, a long flat tail
         x = (rng.standard_normal(n) * 0.1).astype(np.float32)
         x[rng.integers(n)] = 12.0
@@ -88,7 +90,7 @@ def test_sampler_greedy_cases(ext):
 
 
 CASES = [(n, kind, t, k, p) for n, kind in [(8, "normal"), (1000, "grid"), (1000, "special"), (V, "normal"),
-                                            (V, "grid"), (V, "special"), (V, "peaked")]
+                                            (V, "grid"), (V, "special"), (V, "peaked"), (V, "ties")]
          for (t, k, p) in [(1.0, 0, 1.0), (0.7, 50, 1.0), (1.0, 0, 0.9), (0.8, 40, 0.95), (2.0, 3, 0.5)]]
 
 
