@@ -139,7 +139,7 @@ int qwen_generate_until(
  * allocate device memory (code under stream capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. Same
  * arguments, limits and results as launch_ldg_generate_nosync; its exchange
- * workspace is a fixed 1,564,928-byte array in the library's device memory
+ * workspace is a fixed 2,813,184-byte array in the library's device memory
  * (one per GPU, held until the process ends) instead of the allocated one, and
  * memory is cleared with a kernel, never hipMemset. Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (two streams, two threads)
@@ -198,10 +198,11 @@ int qwen_sample(const float* logits, int n, float temperature, int top_k, float 
 /* Sampled generation (no counterpart in the reference): generate_nosync whose
  * every next token comes from qwen_sample over that step's logits (seed,
  * step = the position of the step's input token) instead of the argmax. With
- * temperature alone (top_k 0 and top_p >= 1) the decode kernel's sampling build
- * draws each token itself in one launch of num_steps steps; otherwise it runs
- * as num_steps pairs of launches (a decode step, then the sampler); neither
- * synchronises with the host. With eos_token_id >= 0 the generation ends after the
+ * temperature > 0 and either top_k 0 (or >= 151936) and top_p >= 1 (temperature
+ * alone), or 1 <= top_k <= 128 (any top_p), the decode kernel's sampling build
+ * draws each token itself in one launch of num_steps steps (the same kept set
+ * and draw as qwen_sample); otherwise it runs as num_steps pairs of launches (a
+ * decode step, then the sampler); neither synchronises with the host. With eos_token_id >= 0 the generation ends after the
  * first sampled eos: output_log[0 .. n) holds the sampled ids, eos last when it
  * was reached, later entries are -1, and n = *out_count (device int32,
  * nullable) <= num_steps; the K/V cache holds positions start_position ..
@@ -223,6 +224,15 @@ int qwen_generate_sampled(
  * used as is (no norm), W fp16 [151936, 1024]; logits_out (fp32 [151936]) nullable.
  * Exact ties resolve to the lowest row. */
 int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token,
+                        float* logits_out, hipStream_t stream);
+
+/* Isolated lm_head + top-k draw (no counterpart in the reference): the same
+ * logits as qwen_lm_head_argmax, then the token the decode kernel's sampling
+ * build draws inside a top-k generation (temperature > 0, 1 <= top_k <= 128,
+ * top_p as in qwen_sample; Philox step = position). It equals qwen_sample on
+ * logits_out with the same arguments; it exists to test that in-kernel draw. */
+int qwen_lm_head_sample(const void* hidden_f16, const void* weight, float temperature, int top_k,
+                        float top_p, unsigned long long seed, int position, int* out_token,
                         float* logits_out, hipStream_t stream);
 
 /* Isolated MLP half-layer: y = x + down(silu(gate(n)) * up(n)), n = RMSNorm(x) * post_norm_w,

@@ -37,7 +37,20 @@ int main() {
   }
   CHECK(XCD_SLOTS % 2 == 0 && OFF_ARG % 2 == 0, "xcd / arg alignment");
   CHECK(xbuf(1, NXCD - 1, XCD_SLOTS) == OFF_ARG, "xcd buffers end at the ARG buffer");
-  CHECK(OFF_ARG + 2L * ARG_SLOTS == TOTAL_SLOTS, "ARG end");
+  CHECK(OFF_ARG + 2L * ARG_SLOTS == OFF_LOGIT && OFF_LOGIT + LOGIT_SLOTS == OFF_SEL &&
+            OFF_SEL + SEL_SLOTS == TOTAL_SLOTS, "ARG, LOGIT, SEL end");
+  CHECK(OFF_LOGIT % 2 == 0 && LOGIT_SLOTS % 2 == 0 && OFF_SEL % 2 == 0, "LOGIT / SEL pairs are 16-byte aligned");
+  CHECK(OFF_LOGIT % LM_CHUNK == 0 && slot_logit(0) == OFF_LOGIT && slot_logit(VOCAB - 1) == OFF_LOGIT + VOCAB - 1,
+        "an lm_head chunk's logits are one 64-byte line");
+  CHECK((SL_ROWS - 1) * NWG + SL_FULL == VOCAB && SL_FULL > 0 && SL_FULL <= NWG, "slices cover the vocabulary");
+  {
+    long used = 0;
+    for (int w = 0; w < NWG; ++w) {
+      used += slice_rows(w);
+      CHECK(w + (long)NWG * (slice_rows(w) - 1) < VOCAB && w + (long)NWG * slice_rows(w) >= VOCAB, "slice w's rows");
+    }
+    CHECK(used == VOCAB, "slice sizes sum to the vocabulary");
+  }
   CHECK(TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
   CHECK(BLOCK == 512 && NLOC == 32 && NXCD * NLOC == NWG, "grid constants");
   for (int w = 0; w < NWG; ++w) CHECK(8 * loc_of(w) + xcd_of(w) == w, "w = 8 i + x");

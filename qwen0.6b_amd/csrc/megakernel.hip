@@ -41,6 +41,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 #include <mutex>
 
@@ -109,7 +110,12 @@ struct KParams {
   float temperature;
   u64 seed;
   int sample;              // host side: launch the sampling build
+  // the sampling build with 1 <= top_k <= TOPK_MAX: the token is drawn from the top-k (then
+  // top-p, when top_p < 1) tokens of the step's logits (draw_topk) instead of from all of them
+  int top_k;
+  float top_p;
 };
+constexpr int TOPK_MAX = 128;  // largest top_k the decode kernel draws from itself
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds of two 32x32 -> 64 multiplies
 // with the published multipliers and key increments; returns the first output word
@@ -137,6 +143,27 @@ __device__ __forceinline__ float gumbel(u64 seed, u32 step, u32 j) {
   const float u = ((float)(x >> 9) + 0.5f) * (1.0f / 8388608.0f);
   return -logf(-logf(u));
 }
+
+// order-preserving key: larger floats give larger keys; NaN gives 0 (below -inf)
+__device__ __forceinline__ u32 fkey(float v) {
+  if (v != v) return 0u;
+  const u32 b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(u32 k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// unnormalised probability exp((l - M) / T) in units of 2^-40; 0 for NaN (M is the largest
+// logit, so the value is at most 2^40 and a vocabulary's sum fits 64 bits)
+__device__ __forceinline__ u64 mass(float l, float M, float T) {
+  if (l != l) return 0;
+  return (u64)(expf((l - M) / T) * 1099511627776.0f);
+}
+
+// (key << 32 | ~index): the larger of two is the larger key, then the lower index
+__device__ __forceinline__ u64 pack_best(u32 key, int idx) { return ((u64)key << 32) | (u64)(0xffffffffu - (u32)idx); }
+__device__ __forceinline__ int best_index(u64 b) { return (int)(0xffffffffu - (u32)b); }
 
 // ------------------------------------------------------------------------------------
 // device code: the production kernel, and a copy that records per-stage timestamps
@@ -725,9 +752,10 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
   if (!output_log || first_token_id < 0 || first_token_id >= VOCAB || eos_token_id < -1 || eos_token_id >= VOCAB ||
       !sample_args_ok(temperature, top_k, top_p))
     return QWEN_ERR_ARG;
-  if (temperature > 0.f && (top_k == 0 || top_k >= VOCAB) && !(top_p < 1.f)) {
-    // temperature alone: the decode kernel's sampling build draws every token itself (one
-    // launch, eos checked on the device as in qwen_generate_until)
+  const bool fused_k = temperature > 0.f && top_k >= 1 && top_k <= TOPK_MAX;
+  if (fused_k || (temperature > 0.f && (top_k == 0 || top_k >= VOCAB) && !(top_p < 1.f))) {
+    // temperature alone, or top-k with top_k <= TOPK_MAX: the decode kernel's sampling build
+    // draws every token itself (one launch, eos checked on the device as in qwen_generate_until)
     P.first_token = first_token_id;
     P.out_tokens = output_log;
     P.out_count = out_count;
@@ -735,6 +763,8 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
     P.temperature = temperature;
     P.seed = seed;
     P.sample = 1;
+    P.top_k = fused_k ? top_k : 0;
+    P.top_p = top_p;
     return launch(P, stream);
   }
   char* buf = nullptr;
@@ -796,6 +826,32 @@ extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, i
   P.num_layers = 1;
   P.num_steps = 1;
   P.max_seq = MAX_SEQ_LIMIT;
+  return launch(P, stream);
+}
+
+extern "C" int qwen_lm_head_sample(const void* hidden_f16, const void* weight, float temperature, int top_k,
+                                   float top_p, unsigned long long seed, int position, int* out_token,
+                                   float* logits_out, hipStream_t stream) {
+  if (!hidden_f16 || !weight || !out_token || !aligned16(hidden_f16) || !aligned16(weight)) return QWEN_ERR_ARG;
+  if (logits_out && !aligned16(logits_out)) return QWEN_ERR_ARG;
+  if (!(temperature > 0.f) || top_k < 1 || top_k > TOPK_MAX || top_p != top_p || position < 0) return QWEN_ERR_ARG;
+  KParams P;
+  memset(&P, 0, sizeof(P));
+  P.eos = -1;
+  P.lm_head = (const _Float16*)weight;
+  P.in_vec = (const _Float16*)hidden_f16;
+  P.out_tokens = out_token;
+  P.logits_out = logits_out;
+  P.mode = MODE_LMHEAD;
+  P.num_layers = 1;
+  P.num_steps = 1;
+  P.start_pos = position;
+  P.max_seq = MAX_SEQ_LIMIT;
+  P.temperature = temperature;
+  P.seed = seed;
+  P.sample = 1;
+  P.top_k = top_k;
+  P.top_p = top_p;
   return launch(P, stream);
 }
 

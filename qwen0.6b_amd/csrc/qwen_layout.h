@@ -246,13 +246,30 @@ constexpr long B_INT = B_ACT + ACT_SLOTS;
 constexpr long B_DP = B_INT + INT_SLOTS;
 constexpr long XCD_SLOTS = B_DP + DP_SLOTS;   // 12032 per XCD per parity
 constexpr long OFF_ARG = 2L * NXCD * XCD_SLOTS;
-constexpr long TOTAL_SLOTS = OFF_ARG + 2L * ARG_SLOTS;
+// Top-k sampling inside the decode kernel (its sampling build) adds two buffers, each written
+// once per token (no workgroup reaches the next token's lm_head before every workgroup has
+// finished this token's draw, so one copy suffices):
+//  * LOGIT: the step's logits, F1, one slot per row (an lm_head chunk is one 64-byte line);
+//  * SEL: the SEL_DEPTH largest entries of each slice (slice w: rows w + NWG j, SL_ROWS or
+//    SL_ROWS - 1 of them), in descending (key, lower row) order, as slot pairs
+//    (order-preserving key of the logit, row).
+constexpr int SL_ROWS = (VOCAB + NWG - 1) / NWG;  // 594
+constexpr int SL_FULL = VOCAB - (SL_ROWS - 1) * NWG;  // 128 slices hold SL_ROWS rows
+constexpr int SEL_DEPTH = 8;
+constexpr long OFF_LOGIT = OFF_ARG + 2L * ARG_SLOTS;
+constexpr long LOGIT_SLOTS = VOCAB;
+constexpr long OFF_SEL = OFF_LOGIT + LOGIT_SLOTS;
+constexpr long SEL_SLOTS = 2L * NWG * SEL_DEPTH;   // 4096
+constexpr long TOTAL_SLOTS = OFF_SEL + SEL_SLOTS;
 // after the slots: one 256-byte line of status words, then the lm_head pool counters
 constexpr long WORKSPACE_BYTES = TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES;
 
 // first slot of buffer `b` (one of B_*) of XCD x, parity par
 QL_HD long xbuf(int par, int x, long b) { return ((long)par * NXCD + x) * XCD_SLOTS + b; }
 QL_HD long slot_arg(int par, int k) { return OFF_ARG + (long)par * ARG_SLOTS + k; }
+QL_HD long slot_logit(int row) { return OFF_LOGIT + row; }
+// rows of slice w
+QL_HD int slice_rows(int w) { return w < SL_FULL ? SL_ROWS : SL_ROWS - 1; }
 // PART entry e (0..129) of split s, local q head hh
 QL_HD long part_index(int s, int hh, int e) { return (long)(s * 2 + hh) * PART_PER_HEAD + e; }
 // INT slot holding inter values 12 i + 3 c + {0, 1} (k = 0) or {2, pad} (k = 1)
@@ -262,5 +279,7 @@ QL_HD int int_slot(int i, int c, int k) { return 8 * i + 2 * c + k; }
 // tag = epoch << 8 | layer * 8 + stage id; epoch counts tokens (never 0).
 QL_HD unsigned tag_of(unsigned epoch, int layer, int st) { return (epoch << 8) | (unsigned)(layer * NSTAGE + st); }
 QL_HD unsigned tag_arg(unsigned epoch) { return (epoch << 8) | 255u; }
+QL_HD unsigned tag_logit(unsigned epoch) { return (epoch << 8) | 254u; }
+QL_HD unsigned tag_sel(unsigned epoch) { return (epoch << 8) | 253u; }
 
 }  // namespace ql

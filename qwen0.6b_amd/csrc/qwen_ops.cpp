@@ -277,6 +277,23 @@ torch::Tensor lm_head_argmax(torch::Tensor hidden, torch::Tensor weight, c10::op
   return out;
 }
 
+torch::Tensor lm_head_sample(torch::Tensor hidden, torch::Tensor weight, double temperature, int64_t top_k,
+                             double top_p, uint64_t seed, int64_t position, c10::optional<torch::Tensor> logits_out) {
+  check_dev(hidden, "hidden", torch::kHalf, H);
+  check_dev(weight, "weight", torch::kHalf, V * H);
+  float* lo = nullptr;
+  if (logits_out.has_value()) {
+    check_dev(*logits_out, "logits_out", torch::kFloat, V);
+    lo = logits_out->data_ptr<float>();
+  }
+  TORCH_CHECK(top_k >= 1 && top_k <= 128 && position >= 0 && position < (1LL << 31), "lm_head_sample: top_k in [1, 128]");
+  auto out = torch::zeros({1}, torch::dtype(torch::kInt32).device(weight.device()));
+  check_rc(qwen_lm_head_sample(hidden.data_ptr(), weight.data_ptr(), (float)temperature, (int)top_k, (float)top_p, seed,
+                               (int)position, out.data_ptr<int>(), lo, stream_of(weight)),
+           "lm_head_sample");
+  return out;
+}
+
 torch::Tensor mlp_block(torch::Tensor x, torch::Tensor post_norm, torch::Tensor gate, torch::Tensor up,
                         torch::Tensor down) {
   check_dev(x, "x", torch::kHalf, H);
@@ -330,6 +347,10 @@ PYBIND11_MODULE(qwen_megakernel_C, m) {
         pybind11::arg("attn_scale"));
   m.def("lm_head_argmax", &lm_head_argmax, "isolated lm_head GEMV + argmax", pybind11::arg("hidden"),
         pybind11::arg("weight"), pybind11::arg("logits_out") = pybind11::none());
+  m.def("lm_head_sample", &lm_head_sample, "isolated lm_head GEMV + the decode kernel's top-k draw",
+        pybind11::arg("hidden"), pybind11::arg("weight"), pybind11::arg("temperature"), pybind11::arg("top_k"),
+        pybind11::arg("top_p"), pybind11::arg("seed"), pybind11::arg("position"),
+        pybind11::arg("logits_out") = pybind11::none());
   m.def("mlp_block", &mlp_block, "isolated RMSNorm + SwiGLU MLP + residual");
   m.def("prefill_timestamps", &prefill_timestamps, "wall-clock ticks (100 MHz) at the start and at every grid "
         "barrier of the last prefill: start, embedding, then QKV / attention / o_proj / gate-up / down per layer");

@@ -132,6 +132,99 @@ def test_sampler_distribution(ext):
     assert chisquare(counts[p > 0], p[p > 0] * n).pvalue > 1e-4
 
 
+# ---- the decode kernel's own top-k draw, on chosen logits ---------------------------------
+# qwen_lm_head_sample runs the lm_head and that draw alone: with the input vector e_0 (fp16 1.0)
+# and lm_head column 0 set to fp16 values x (the other columns 0), the logits are exactly x.
+
+
+def _fast_path_holds(x, top_k):
+    """Whether the in-kernel draw can decide from the slices' 8 largest entries (slice w: rows
+    w + 256 j): every slice's 8th largest key below the k-th largest key of those entries."""
+    keys = sp.fkey(x).astype(np.int64)
+    rows = np.arange(V)
+    published, last = [], []
+    for w in range(256):
+        idx = rows[w::256]
+        top = idx[np.lexsort((idx, -keys[idx]))[:8]]
+        published.extend(keys[top])
+        last.append(keys[top[7]])
+    vk = np.sort(np.array(published))[::-1][top_k - 1]
+    return max(last) < vk
+
+
+def _chosen_logits(kind, rng):
+    x = (rng.standard_normal(V) * 3).astype(np.float16)
+    if kind == "cluster":  # the 24 largest logits all in slice 5: more than 8 of any top-k there
+        order = np.argsort(-x.astype(np.float32), kind="stable")
+        rows = 5 + 256 * rng.choice(V // 256, 24, replace=False)
+        big = x[order[:24]].copy()
+        x[order[:24]] = x[rows]
+        x[rows] = big
+    elif kind == "flat":  # every logit equal but a few: the top-k boundary tie is the vocabulary
+        x[:] = np.float16(0.5)
+        x[rng.choice(V, 5, replace=False)] = np.float16(2.0)
+    elif kind == "grid":  # many exact ties at every cut
+        x = np.round(x.astype(np.float32) / 2).astype(np.float16)
+    elif kind == "special":  # NaN and -inf logits are never drawn
+        idx = rng.choice(V, 4000, replace=False)
+        x[idx[:2000]] = np.float16(np.nan)
+        x[idx[2000:]] = -np.inf
+    elif kind == "inf":  # a +inf logit: the draw is the argmax
+        x[rng.integers(V)] = np.inf
+    return x
+
+
+@pytest.fixture(scope="module")
+def lm_e0():
+    w = torch.zeros((V, 1024), dtype=torch.float16, device="cuda")
+    h = torch.zeros(1024, dtype=torch.float16, device="cuda")
+    h[0] = 1.0
+    return w, h
+
+
+@pytest.mark.parametrize("kind", ["normal", "cluster", "flat", "grid", "special", "inf"])
+def test_in_kernel_topk_draw_matches_oracle(ext, lm_e0, kind):
+    """The decode kernel's top-k draw (fast path from the slices' published entries, full path
+    over every logit otherwise) picks the oracle's token on the same logits, up to the same
+    exemptions as the sampler kernel; "cluster" and "flat" can only be decided by the full path."""
+    w, h = lm_e0
+    rng = np.random.default_rng(len(kind) * 1000 + 17)
+    x16 = _chosen_logits(kind, rng)
+    w[:, 0] = torch.from_numpy(x16).cuda()
+    lo = torch.empty(V, dtype=torch.float32, device="cuda")
+    params = [(0.7, 50, 1.0), (0.8, 40, 0.95), (2.0, 3, 0.5), (1.0, 128, 0.9), (1.0, 1, 1.0), (0.5, 2, 0.0)]
+    paths = set()
+    exempt = 0
+    for temperature, top_k, top_p in params:
+        fast = _fast_path_holds(x16.astype(np.float32), top_k)
+        paths.add(fast)
+        if kind in ("cluster", "flat") and top_k > 8:
+            assert not fast
+        for d in range(4):
+            seed, pos = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**31 - 1))
+            got = int(ext.lm_head_sample(h, w, temperature, top_k, top_p, seed, pos, lo).item())
+            x = lo.cpu().numpy()
+            assert np.array_equal(x, x16.astype(np.float32), equal_nan=True)
+            want, info = sp.sample(x, temperature, top_k, top_p, seed, pos, details=True)
+            if got != want and _exempt(info):
+                exempt += 1
+                continue
+            assert got == want, f"{kind} T {temperature} k {top_k} p {top_p} seed {seed} pos {pos}: " \
+                                f"device {got}, oracle {want} ({info}), fast path {fast}"
+    assert exempt <= 2
+    if kind == "normal":
+        assert True in paths
+    if kind in ("cluster", "flat"):
+        assert False in paths
+
+
+def test_in_kernel_topk_draw_errors(ext, lm_e0):
+    w, h = lm_e0
+    for t, k in [(0.0, 5), (1.0, 0), (1.0, 129)]:
+        with pytest.raises(RuntimeError):
+            ext.lm_head_sample(h, w, t, k, 1.0, 1, 0)
+
+
 class State:
     def __init__(self, w, packed):
         self.w, self.packed = w, packed
@@ -173,8 +266,11 @@ def _prefilled(full, ext):
     return st
 
 
+# (0.8, 50, 0.95), (0.7, 3, 0.5), (1.0, 128, 1.0) and temperature alone are drawn inside the
+# decode kernel; top-p alone and top_k > 128 by the sampler kernel after each decode step
 @pytest.mark.parametrize("temperature,top_k,top_p,seed", [(0.8, 50, 0.95, 1234), (1.5, 0, 1.0, 99),
-                                                          (1.0, 0, 0.7, 2**63 + 5)])
+                                                          (1.0, 0, 0.7, 2**63 + 5), (0.7, 3, 0.5, 5),
+                                                          (1.0, 128, 1.0, 8), (0.9, 200, 1.0, 7)])
 def test_generate_sampled_matches_replay(ext, full, temperature, top_k, top_p, seed):
     """24 sampled steps after a 16-id prompt; the same ids teacher forced give every step's
     logits bit for bit, from which the sampler (device, and oracle up to exemptions) picks
@@ -219,22 +315,23 @@ def test_generate_sampled_seeds(ext, full):
     assert runs[0] != runs[2]
 
 
-def test_generate_sampled_ends_at_eos(ext, full):
+@pytest.mark.parametrize("top_k,top_p", [(0, 1.0), (40, 0.9)])
+def test_generate_sampled_ends_at_eos(ext, full, top_k, top_p):
     start, n = len(PROMPT) - 1, 24
-    ids, _ = _prefilled(full, ext).sampled(ext, PROMPT[-1], n, start, 1.2, 0, 1.0, 31)
+    ids, _ = _prefilled(full, ext).sampled(ext, PROMPT[-1], n, start, 1.2, top_k, top_p, 31)
     cut = next(i for i in range(3, n) if ids[i] not in ids[:i])
     st = _prefilled(full, ext)
-    out, count = st.sampled(ext, PROMPT[-1], n, start, 1.2, 0, 1.0, 31, eos=ids[cut])
+    out, count = st.sampled(ext, PROMPT[-1], n, start, 1.2, top_k, top_p, 31, eos=ids[cut])
     assert count == cut + 1
     assert out[:count] == ids[:count] and out[count:] == [-1] * (n - count)
     # the cache up to the eos step is that of the run without eos
     ref = _prefilled(full, ext)
-    ref.sampled(ext, PROMPT[-1], count, start, 1.2, 0, 1.0, 31)
+    ref.sampled(ext, PROMPT[-1], count, start, 1.2, top_k, top_p, 31)
     e = start + count
     assert torch.equal(st.kc[:, :, :e], ref.kc[:, :, :e]) and torch.equal(st.vc[:, :, :e], ref.vc[:, :, :e])
     # the next call starts afresh (the stop mark of the previous generation is not inherited)
     # and continues the run from the eos position as if it had not stopped
-    again, c2 = st.sampled(ext, ids[cut], n - count, e, 1.2, 0, 1.0, 31)
+    again, c2 = st.sampled(ext, ids[cut], n - count, e, 1.2, top_k, top_p, 31)
     assert c2 == n - count and again == ids[count:]
 
 
