@@ -51,6 +51,8 @@ _OPS = ("decode", "generate_nosync", "generate_until")
 
 # sampled generation with an eos id: steps enqueued between two host checks for the eos
 SAMPLED_CHUNK = 32
+# largest top_k the decode kernel draws from itself (a sampled generation is then one launch)
+TOPK_IN_KERNEL = 128
 
 
 def _require_megakernel_op(op_name: str):
@@ -377,17 +379,21 @@ class Decoder:
         synchronisation until the end: each step's next token is drawn on the device from
         its logits (temperature, then top-k, then top-p, then a draw seeded by ``seed`` and
         the step's position; temperature <= 0 or top_k == 1 is greedy). With
-        ``eos_token_id`` the generation ends after that id (which ends the list), checked
-        on the host every ``SAMPLED_CHUNK`` steps (the steps enqueued after an eos are
-        wasted work); advances the position by the number of steps run."""
+        ``eos_token_id`` the generation ends after that id (which ends the list): on the
+        device when the decode kernel draws the tokens itself (temperature alone, or
+        1 <= top_k <= ``TOPK_IN_KERNEL``), else checked on the host every ``SAMPLED_CHUNK``
+        steps (the steps enqueued after an eos are wasted work); advances the position by
+        the number of steps run."""
         if self._position + max_tokens > MAX_SEQ_LEN:
             raise RuntimeError(f"positions {self._position}..{self._position + max_tokens} exceed {MAX_SEQ_LEN}")
         if top_k < 0 or not 0.0 <= top_p or temperature != temperature:
             raise ValueError(f"invalid sampling parameters temperature={temperature} top_k={top_k} top_p={top_p}")
         gen = _require_megakernel_op("generate_sampled")
         eos = -1 if eos_token_id is None else int(eos_token_id)
-        # temperature alone runs as one launch that checks eos on the device: no chunking
-        one_launch = top_k == 0 and top_p >= 1.0
+        # temperature alone, and top-k up to TOPK_IN_KERNEL, run as one launch that checks eos
+        # on the device: no chunking
+        one_launch = temperature > 0 and (((top_k == 0 or top_k >= VOCAB_SIZE) and top_p >= 1.0)
+                                          or 1 <= top_k <= TOPK_IN_KERNEL)
         chunk = max_tokens if eos < 0 or one_launch else SAMPLED_CHUNK
         out, first = [], int(first_token_id)
         while len(out) < max_tokens:

@@ -251,12 +251,14 @@ def _sampled_ref(hw, prompt, n, eos=None, **kw):
 
 
 def test_generate_ids_sampled_chunks_and_eos(qa_cpu, small_hw):
-    """temperature > 0 goes to generate_sampled; with an eos id the Decoder enqueues
-    SAMPLED_CHUNK steps at a time, continues from the last id and position, and stops
-    after the eos; the draws depend on the position only, so chunking changes nothing."""
+    """temperature > 0 goes to generate_sampled; with an eos id and top-p alone (a decode
+    launch and a sampler launch per step) the Decoder enqueues SAMPLED_CHUNK steps at a
+    time, continues from the last id and position, and stops after the eos; the draws depend
+    on the position only, so chunking changes nothing. With top-k the decode kernel draws
+    the tokens and stops at the eos itself: one call."""
     mod, stub = qa_cpu
     mod.SAMPLED_CHUNK = 3
-    kw = dict(temperature=1.3, top_k=20, top_p=0.9, seed=77)
+    kw = dict(temperature=1.3, top_k=0, top_p=0.9, seed=77)
     prompt = [3, 1, 4, 1, 5]
     ref = _sampled_ref(small_hw, prompt, 10, **kw)
     dec = mod.Decoder(weights=_weights(mod), verbose=False)
@@ -271,6 +273,14 @@ def test_generate_ids_sampled_chunks_and_eos(qa_cpu, small_hw):
     sampled = [c for c in stub.calls if c[0] == "generate_sampled"]
     assert [c[2] for c in sampled] == list(range(4, 4 + k + 1, 3))  # chunk starts
     assert all(c[1] == (5 if i == 0 else ref[3 * i - 1]) for i, c in enumerate(sampled))
+    # top-k (and temperature alone) in one call, eos included
+    for kk in (dict(temperature=1.3, top_k=20, top_p=0.9, seed=77), dict(temperature=1.3, top_k=0, top_p=1.0, seed=5)):
+        ref2 = _sampled_ref(small_hw, prompt, 10, **kk)
+        k2 = next(i for i in range(4, 10) if ref2[i] not in ref2[:i])
+        stub.oracle.reset()
+        stub.calls.clear()
+        assert dec.generate_ids(prompt, 10, eos_token_id=ref2[k2], **kk) == ref2[:k2 + 1]
+        assert [c for c in stub.calls if c[0] == "generate_sampled"] == [("generate_sampled", 5, 4, 10, ref2[k2])]
     # greedy settings take the greedy path
     stub.calls.clear()
     stub.oracle.reset()
