@@ -296,6 +296,32 @@ def test_generate_sampled_matches_replay(ext, full, temperature, top_k, top_p, s
     assert ids != [int(np.argmax(lo[s])) for s in range(n)]
 
 
+def test_generate_sampled_long_replay_at_bench_shape(ext, full):
+    """The sampled benchmark's shape: a 1000-id prompt prefilled, then 256 steps (positions
+    999..1254) drawn inside the decode kernel with temperature 0.8, top-k 50, top-p 0.95. The
+    same ids teacher forced give every step's logits, from which the sampler kernel picks
+    exactly the run's ids; the K/V caches of the two runs are identical."""
+    temperature, top_k, top_p, seed, n = 0.8, 50, 0.95, 7, 256
+    prompt = [int(t) for t in np.random.default_rng(11).integers(0, V, 1000)]
+    start = len(prompt) - 1
+    runs = []
+    for _ in range(2):
+        st = State(*full)
+        f = torch.tensor(prompt[:-1], dtype=torch.int32, device="cuda")
+        w = st.w
+        ext.prefill(f, w["embed_weight"], st.packed, w["cos_table"], w["sin_table"], st.kc, st.vc, st.hidden, 28, 0,
+                    MAX_SEQ, SCALE)
+        torch.cuda.synchronize()
+        assert ext.last_error() == 0
+        runs.append(st)
+    ids, count = runs[0].sampled(ext, prompt[-1], n, start, temperature, top_k, top_p, seed)
+    assert count == n and all(0 <= t < V for t in ids)
+    _, lo = runs[1].forced(ext, [prompt[-1]] + ids[:-1], start, logits=True)
+    again = torch.cat([ext.sample(lo[s], temperature, top_k, top_p, seed, start + s) for s in range(n)])
+    assert again.cpu().tolist() == ids
+    assert torch.equal(runs[0].kc, runs[1].kc) and torch.equal(runs[0].vc, runs[1].vc)
+
+
 def test_generate_sampled_greedy_settings_equal_greedy(ext, full):
     start, n = len(PROMPT) - 1, 20
     st = _prefilled(full, ext)
