@@ -164,7 +164,7 @@ int qwen_generate_nosync_noalloc(
  * a prompt comes from a decode step of its last id. Ids outside [0, 151936)
  * are reported by qwen_last_error() (QWEN_ERR_BAD_TOKEN). A prompt prefilled
  * in pieces (each at its own start position) leaves the same K/V cache, bit for
- * bit, as one call with all of it. Allocates a 114 MB workspace per device on
+ * bit, as one call with all of it. Allocates a 78 MB workspace per device on
  * first use (activations of up to 2048 positions, partial attention results). */
 int qwen_prefill(
     const int* ids, int n, const void* embed_weight,

@@ -411,8 +411,8 @@ constexpr long PF_BYTES = PF_PART + 4L * pf::MAX_PSLOTS * NKV * pf::PART_FLOATS;
 static_assert(PF_BAR_BYTES % 4 == 0 && PF_PART % 256 == 0, "prefill workspace alignment");
 
 // The attention work of a prefill of n positions from position start: query block b (positions
-// start + 32 b ..) reads key blocks 0 .. nkb(b) - 1 (64 keys each, causal), in chunks of 8 key
-// blocks; a block with more than one chunk is split into units (the kernel merges their partial
+// start + 32 b ..) reads key blocks 0 .. nkb(b) - 1 (64 keys each, causal), in chunks of
+// pf::KCHUNK key blocks; a block with more than one chunk is split into units (the kernel merges their partial
 // results). Units are sorted longest first (ties: later query block first, then chunk order),
 // the order in which the kernel deals them out.
 static int prefill_units(int n, int start, pf::PParams& P) {
