@@ -67,7 +67,8 @@ def cpu_baseline(hw, budget_s=12.0, max_steps=400):
     """The fp32 CPU oracle decoding at context ~1921 on this host's cores.
     The oracle's KV cache for positions < 1920 is filled with seeded random
     values (decode time does not depend on them); steps are timed after one
-    warm-up step until `budget_s` of work or `max_steps` steps."""
+    warm-up step until `budget_s` of work, `max_steps` steps or the end of the
+    cache (positions up to its last, 2047), whichever comes first."""
     import torch
 
     from oracle import qwen3_oracle as orc
@@ -77,6 +78,7 @@ def cpu_baseline(hw, budget_s=12.0, max_steps=400):
     g = torch.Generator().manual_seed(5)
     oracle.k_cache[:, :, :PREFILL] = torch.randn(oracle.k_cache[:, :, :PREFILL].shape, generator=g)
     oracle.v_cache[:, :, :PREFILL] = torch.randn(oracle.v_cache[:, :, :PREFILL].shape, generator=g)
+    max_steps = min(max_steps, oracle.k_cache.shape[2] - PREFILL - 1)  # positions PREFILL + 1 .. 2047
     tok = 1234
     out = oracle.step(tok, PREFILL)  # warm-up
     tok = out["token"]

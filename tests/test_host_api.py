@@ -328,3 +328,14 @@ def test_load_weights_reads_safetensors(qa_cpu, tmp_path):
             assert t.dtype == torch.float16 and float(t[0]) == float(i * 11 + j)
     assert w["lm_head_weight"] is w["embed_weight"]
     assert w["cos_table"].shape == (mod.MAX_SEQ_LEN, mod.HEAD_DIM) and w["cos_table"].dtype == torch.float16
+
+
+def test_bench_cpu_baseline_stays_inside_the_cache(monkeypatch):
+    """bench.py's CPU baseline times oracle decode steps from position PREFILL + 1 until its time
+    budget or step limit, and never past the cache's last position (2047), however fast the host."""
+    import bench
+
+    monkeypatch.setattr(bench, "PREFILL", 2040)
+    hw = qw.host_weights(seed=0, std=0.02)
+    r = bench.cpu_baseline(hw, budget_s=300.0, max_steps=400)
+    assert r["sample"].startswith("7 greedy decode steps") and "positions 2041..2047" in r["sample"], r
