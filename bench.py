@@ -346,7 +346,8 @@ def run_generate_e2e(args):
     if sampling:
         cfg.update(sampling)
         what = ("temperature 0.8, top-k 50, top-p 0.95" if "top_k" in sampling else "temperature 0.8")
-        kernels = "sampled::qwen_decode_kernel"  # top-k <= 128 and temperature alone: drawn inside it
+        # drawn inside the decode kernel: its top-k build, or its temperature-only build
+        kernels = "sampled::qwen_decode_kernel" if "top_k" in sampling else "tsampled::qwen_decode_kernel"
         return aux_line(f"Decoder.generate tokens/sec with sampling ({what}), 1000-id prompt + 1000 new tokens, "
                         "prefill included", round(n_new / ms * 1e3, 2), "tokens/s", True, args.workload, cfg,
                         kernels + " + pf::qwen_prefill_kernel", algorithmic_bytes(n_prompt - 1, n_new), ms,

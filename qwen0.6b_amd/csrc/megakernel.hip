@@ -171,20 +171,32 @@ __device__ __forceinline__ int best_index(u64 b) { return (int)(0xffffffffu - (u
 namespace fast {
 constexpr bool kTrace = false;
 constexpr bool kSample = false;
+constexpr bool kTopK = false;
 #include "decode_body.inc"
 }  // namespace fast
 
 namespace traced {
 constexpr bool kTrace = true;
 constexpr bool kSample = false;
+constexpr bool kTopK = false;
 #include "decode_body.inc"
 }  // namespace traced
 
 namespace sampled {
 constexpr bool kTrace = false;
 constexpr bool kSample = true;
+constexpr bool kTopK = true;
 #include "decode_body.inc"
 }  // namespace sampled
+
+// temperature alone: the sampling build without the top-k draw, whose code would otherwise
+// share (and reshape) this kernel's register allocation
+namespace tsampled {
+constexpr bool kTrace = false;
+constexpr bool kSample = true;
+constexpr bool kTopK = false;
+#include "decode_body.inc"
+}  // namespace tsampled
 
 // the batched prefill kernel (namespace pf)
 #include "prefill_body.inc"
@@ -307,13 +319,13 @@ int device_state(DeviceState** out) {
               prop.gcnArchName, prop.multiProcessorCount);
       return st.err;
     }
-    int occ = 0;
-    int occ_t = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)fast::qwen_decode_kernel, BLOCK, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ_t, (const void*)traced::qwen_decode_kernel, BLOCK, 0) !=
-            hipSuccess ||
-        occ_t < 1 || occ < 1)
-      return st.err;
+    // every build of the decode kernel must fit one workgroup per CU
+    const void* builds[] = {(const void*)fast::qwen_decode_kernel, (const void*)traced::qwen_decode_kernel,
+                            (const void*)sampled::qwen_decode_kernel, (const void*)tsampled::qwen_decode_kernel};
+    for (const void* k : builds) {
+      int occ = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k, BLOCK, 0) != hipSuccess || occ < 1) return st.err;
+    }
     int clk_khz = 0;
     if (hipDeviceGetAttribute(&clk_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || clk_khz <= 0)
       clk_khz = 100000;
@@ -382,7 +394,8 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
   w.epoch = (u32)next;
   void* args[] = {&P};
   const void* kernel = P.trace    ? (const void*)traced::qwen_decode_kernel
-                       : P.sample ? (const void*)sampled::qwen_decode_kernel
+                       : P.sample ? (P.top_k > 0 ? (const void*)sampled::qwen_decode_kernel
+                                                 : (const void*)tsampled::qwen_decode_kernel)
                                   : (const void*)fast::qwen_decode_kernel;
   if (hipLaunchCooperativeKernel(kernel, dim3(NWG), dim3(BLOCK), args, 0, stream) != hipSuccess)
     return QWEN_ERR_LAUNCH;
