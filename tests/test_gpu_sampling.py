@@ -296,12 +296,14 @@ def test_generate_sampled_matches_replay(ext, full, temperature, top_k, top_p, s
     assert ids != [int(np.argmax(lo[s])) for s in range(n)]
 
 
-def test_generate_sampled_long_replay_at_bench_shape(ext, full):
-    """The sampled benchmark's shape: a 1000-id prompt prefilled, then 256 steps (positions
-    999..1254) drawn inside the decode kernel with temperature 0.8, top-k 50, top-p 0.95. The
-    same ids teacher forced give every step's logits, from which the sampler kernel picks
-    exactly the run's ids; the K/V caches of the two runs are identical."""
-    temperature, top_k, top_p, seed, n = 0.8, 50, 0.95, 7, 256
+@pytest.mark.parametrize("top_k,top_p", [(50, 0.95), (0, 1.0)])
+def test_generate_sampled_long_replay_at_bench_shape(ext, full, top_k, top_p):
+    """The sampled benchmarks' shape: a 1000-id prompt prefilled, then 256 steps (positions
+    999..1254) drawn inside the decode kernel with temperature 0.8 and top-k 50, top-p 0.95 (the
+    top-k build) or nothing else (the temperature-only build). The same ids teacher forced give
+    every step's logits, from which the sampler kernel picks exactly the run's ids; the K/V caches
+    of the two runs are identical."""
+    temperature, seed, n = 0.8, 7, 256
     prompt = [int(t) for t in np.random.default_rng(11).integers(0, V, 1000)]
     start = len(prompt) - 1
     runs = []
