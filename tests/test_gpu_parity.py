@@ -263,9 +263,9 @@ def test_batched_prefill_chunked_equals_whole(ext, full, n, cuts):
     cache the earlier pieces wrote) gives the same K/V cache, bit for bit, as one prefill
     of all n: every position's arithmetic is the same in both, whatever tile or query
     block it lands in. At n = 1300 the later query blocks read up to 21 key blocks, so
-    their attention is split into key chunks (8 blocks each) in both runs, with query
+    their attention is split into key chunks (16 blocks of 64 keys each) in both runs, with query
     blocks aligned differently in the pieces (starts 77 and 900). At n = 2047 the last piece is
-    7 ids at position 2040, whose keys split into four chunks."""
+    7 ids at position 2040, whose 32 key blocks split into two chunks."""
     hw, w, packed = full
     ids = qw.synthetic_prompt(n, seed=61)
     a, b = Run(w, packed, 28), Run(w, packed, 28)
