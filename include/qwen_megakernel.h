@@ -136,12 +136,14 @@ int qwen_generate_until(
     int max_seq_len, float attn_scale, hipStream_t stream);
 
 /* launch_ldg_generate_nosync without any allocation, for callers that cannot
- * allocate device memory (code under stream capture, tight serving loops,
- * harnesses that forbid hipMalloc). No counterpart in the reference. Same
- * arguments, limits and results as launch_ldg_generate_nosync; its exchange
- * workspace is a fixed 2,813,184-byte array in the library's device memory
- * (one per GPU, held until the process ends) instead of the allocated one, and
- * memory is cleared with a kernel, never hipMemset. Every call on a GPU shares
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments, limits and
+ * results as launch_ldg_generate_nosync; its exchange workspace is a fixed
+ * 2,813,184-byte array in the library's device memory (one per GPU, held until
+ * the process ends) instead of the allocated one, and memory is cleared with a
+ * kernel, never hipMemset. Not for stream capture: on a stream that is being
+ * captured it returns QWEN_ERR_ARG (the exchange tags' token epochs are launch
+ * arguments, so a replayed graph would reuse them). Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (two streams, two threads)
  * race and must be serialized by the caller. Errors are reported by
  * qwen_last_error(). */
@@ -269,7 +271,10 @@ int qwen_abi_version(void);
  * stage input, 1 = has its quarter of the input, 2 = passed the compute-wave
  * barrier, 3 = stored its results. Pass buf = NULL to stop. While tracing, the
  * launches run a second build of the kernel that carries the trace points (a few
- * microseconds per token slower); without it, the kernel has none. */
+ * microseconds per token slower); without it, the kernel has none. That build
+ * decodes greedily: while tracing, the entry points that draw tokens inside
+ * the decode kernel (qwen_generate_sampled's single-launch forms,
+ * qwen_lm_head_sample) return QWEN_ERR_ARG. */
 int qwen_set_trace(unsigned long long* buf, long long elems, int token);
 int qwen_trace_events(void);
 

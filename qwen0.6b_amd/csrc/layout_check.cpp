@@ -425,6 +425,31 @@ int main() {
     CHECK(tag_of(1, 0, 0) != 0 && tag_arg(1) != 0, "tags of epoch >= 1 are never 0");
   }
 
+  // ---- 64-bit pointers through the 32-bit lane broadcast (readfirstlane: int -> int) ----
+  // Device addresses whose low word has bit 31 set are where a signed broadcast result,
+  // widened straight to 64 bits, would corrupt the high word; every such case is checked
+  // here instead of relying on the allocator to hand one out on the GPU.
+  {
+    auto bcast = [](int x) -> int { return x; };  // host stand-in: same signature as readfirstlane
+    const unsigned long long his[] = {0x0ull, 0x1ull, 0x7f12ull, 0x7fffull, 0xffffffffull};
+    const unsigned long long los[] = {0x0ull, 0x1000ull, 0x7fffffffull, 0x80000000ull, 0x80001234ull,
+                                      0xc0000000ull, 0xfffff000ull, 0xffffffffull};
+    int widened_wrong = 0;
+    for (unsigned long long hi : his)
+      for (unsigned long long lo : los) {
+        const unsigned long long v = (hi << 32) | lo;
+        CHECK(uniform_u64(v, bcast) == v, "uniform_u64(%llx)", v);
+        const U32Pair h = uniform_halves(v, bcast);
+        CHECK(h.lo == (unsigned)lo && h.hi == (unsigned)hi, "uniform_halves(%llx)", v);
+        // the mistake the helper avoids: the signed low half widened to 64 bits before the OR
+        const unsigned long long naive =
+            ((unsigned long long)(unsigned)bcast((int)(unsigned)(v >> 32)) << 32) | (unsigned long long)(long long)bcast((int)(unsigned)v);
+        widened_wrong += naive != v;
+      }
+    // (a high word of all ones hides it: 5 low words >= 2^31 times the 4 other high words)
+    CHECK(widened_wrong == 5 * 4, "the naive join fails exactly for low words >= 2^31 (%d)", widened_wrong);
+  }
+
   if (g_fail) {
     fprintf(stderr, "layout_check: %d failures\n", g_fail);
     return 1;

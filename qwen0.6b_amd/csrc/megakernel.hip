@@ -259,24 +259,9 @@ struct DeviceState {
 
 std::mutex g_mu;
 DeviceState g_dev[MAX_DEVICES];
-std::once_flag g_teardown_once;
-
-// At process exit, before the HIP runtime's own teardown (registered earlier, so run
-// later): wait for the device and free what the library allocated.
-void teardown() {
-  std::lock_guard<std::mutex> lock(g_mu);
-  for (int d = 0; d < MAX_DEVICES; ++d) {
-    DeviceState& st = g_dev[d];
-    if (!st.heap.ws && !st.tab && !st.pf && !st.smp) continue;
-    if (hipSetDevice(d) != hipSuccess) continue;
-    (void)hipDeviceSynchronize();
-    if (st.heap.ws) (void)hipFree(st.heap.ws);
-    if (st.tab) (void)hipFree(st.tab);
-    if (st.pf) (void)hipFree(st.pf);
-    if (st.smp) (void)hipFree(st.smp);
-    st = DeviceState();
-  }
-}
+// What the library allocates (workspaces, the MLP block's pointer table, the prefill and
+// sampler buffers) is held until the process ends and released with it; no exit handler
+// calls into the HIP runtime.
 
 int zero_words(void* p, long bytes, hipStream_t s) {
   hipLaunchKernelGGL(qwen_zero_words, dim3(NWG), dim3(256), 0, s, (u64*)p, bytes / 8);
@@ -357,7 +342,6 @@ int heap_workspace(DeviceState* st) {
   if (st->heap.ws) return QWEN_OK;
   void* p = nullptr;
   if (hipMalloc(&p, WORKSPACE_BYTES) != hipSuccess) return QWEN_ERR_LAUNCH;
-  std::call_once(g_teardown_once, [] { std::atexit(teardown); });
   if (hipMemset(p, 0, WORKSPACE_BYTES) != hipSuccess) {
     (void)hipFree(p);
     return QWEN_ERR_LAUNCH;
@@ -378,6 +362,8 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
   Workspace& w = fixed ? st->fixed : st->heap;
   // a trace buffer must hold every stage of every workgroup of this launch's layers
   if (st->trace && (long long)NWG * trace_stages(P.num_layers) * TRACE_EVENTS > st->trace_elems) return QWEN_ERR_ARG;
+  // the traced build is the greedy kernel: a sampled launch while tracing would return argmax ids
+  if (st->trace && P.sample) return QWEN_ERR_ARG;
   P.ws = w.ws;
   P.status = w.status;
   P.deadline = st->deadline;
@@ -624,7 +610,8 @@ extern "C" int launch_ldg_generate_nosync(int first_token_id, int num_steps, con
 
 // launch_ldg_generate_nosync on the device's fixed `scratch` workspace: no allocation in this
 // call or in its first-use set-up on a device. The workspace need does not depend on the
-// arguments; their limits are those of launch_ldg_generate_nosync (QWEN_ERR_ARG beyond them).
+// arguments; their limits are those of launch_ldg_generate_nosync (QWEN_ERR_ARG beyond them,
+// and on a stream that is being captured).
 extern "C" int qwen_generate_nosync_noalloc(int first_token_id, int num_steps, const void* embed_weight,
                                             const LDGLayerWeight* layer_weights, const void* final_norm_weight,
                                             const void* lm_head_weight, const void* cos_table,
@@ -639,6 +626,11 @@ extern "C" int qwen_generate_nosync_noalloc(int first_token_id, int num_steps, c
                        max_seq_len, attn_scale);
   if (rc != QWEN_OK) return rc;
   if (!output_log || first_token_id < 0 || first_token_id >= VOCAB) return QWEN_ERR_ARG;
+  // Not for stream capture: the tags' token epochs are kernel arguments, so a replayed graph
+  // would reuse them against slots that already carry them, and a device's first call
+  // synchronises with the host (placement probe).
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return QWEN_ERR_ARG;
   P.first_token = first_token_id;
   P.out_tokens = output_log;
   return launch(P, stream, /*fixed=*/true);
@@ -888,7 +880,6 @@ extern "C" int qwen_mlp_block(const void* x_f16, const void* post_norm_weight, c
     int rc = device_state(&st);
     if (rc != QWEN_OK) return rc;
     if (!st->tab && hipMalloc(&st->tab, sizeof(LDGLayerWeight)) != hipSuccess) return QWEN_ERR_LAUNCH;
-    std::call_once(g_teardown_once, [] { std::atexit(teardown); });
     tab = st->tab;
   }
   if (hipMemcpyAsync(tab, &h, sizeof(h), hipMemcpyHostToDevice, stream) != hipSuccess) return QWEN_ERR_LAUNCH;

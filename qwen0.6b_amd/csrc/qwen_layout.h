@@ -282,4 +282,25 @@ QL_HD unsigned tag_arg(unsigned epoch) { return (epoch << 8) | 255u; }
 QL_HD unsigned tag_logit(unsigned epoch) { return (epoch << 8) | 254u; }
 QL_HD unsigned tag_sel(unsigned epoch) { return (epoch << 8) | 253u; }
 
+// ---- 64-bit values through a 32-bit lane broadcast -----------------------------------
+// `bcast` stands for the GPU's readfirstlane, which takes and returns a signed int. Each
+// half of v is broadcast on its own and read back through unsigned, so a low half with
+// bit 31 set is not sign-extended into the high half when the two are joined (casting the
+// signed result straight to 64 bits would OR 0xffffffff into the high word).
+struct U32Pair {
+  unsigned lo, hi;
+};
+template <typename B>
+QL_HD U32Pair uniform_halves(unsigned long long v, B bcast) {
+  U32Pair r;
+  r.lo = (unsigned)bcast((int)(unsigned)v);
+  r.hi = (unsigned)bcast((int)(unsigned)(v >> 32));
+  return r;
+}
+template <typename B>
+QL_HD unsigned long long uniform_u64(unsigned long long v, B bcast) {
+  const U32Pair h = uniform_halves(v, bcast);
+  return ((unsigned long long)h.hi << 32) | (unsigned long long)h.lo;
+}
+
 }  // namespace ql

@@ -225,6 +225,23 @@ def test_in_kernel_topk_draw_errors(ext, lm_e0):
             ext.lm_head_sample(h, w, t, k, 1.0, 1, 0)
 
 
+def test_sampling_refused_while_tracing(ext, lm_e0):
+    """The traced build decodes greedily: a draw inside the decode kernel while tracing is
+    refused rather than answered with the argmax; the same call works again once tracing stops."""
+    w, h = lm_e0
+    w[:, 0] = torch.linspace(-1, 1, V, device="cuda").to(torch.float16)
+    buf = torch.zeros(256 * 9 * ext.trace_events(), dtype=torch.int64, device="cuda")
+    ext.set_trace(buf, 0)
+    try:
+        with pytest.raises(RuntimeError):
+            ext.lm_head_sample(h, w, 0.8, 50, 0.95, 3, 7)
+    finally:
+        ext.set_trace(None, 0)
+    got = int(ext.lm_head_sample(h, w, 0.8, 50, 0.95, 3, 7).item())
+    assert 0 <= got < V
+    assert ext.last_error() == 0
+
+
 class State:
     def __init__(self, w, packed):
         self.w, self.packed = w, packed

@@ -4,9 +4,12 @@ launch_ldg_generate_nosync, both through the C-ABI (ctypes).
 Two calls of the no-allocation entry point in a row, the second smaller (fewer
 steps, another first token), are compared bit for bit with the allocating
 entry point on the same inputs: generated ids, the final hidden state,
-norm_out and the whole K/V cache. In a fresh process the no-allocation entry
-point is the library's first call, so its device set-up runs without any
-allocation.
+norm_out and the whole K/V cache. The device's free memory is the same before
+and after those calls (their output buffers are made first). Run after the
+other GPU tests (the usual order), the library's per-device set-up has already
+happened; run alone in a fresh process, the first of these calls does it, and
+that set-up allocates nothing either (a placement probe written into the
+fixed array). Under stream capture the entry point is refused.
 """
 
 import ctypes
@@ -56,10 +59,14 @@ class State:
                      self.norm_out.data_ptr(), u, u]
 
 
-def _run(lib, name, w, packed, first, n):
-    st = State(w, packed, n)
-    rc = getattr(lib, name)(first, n, *st.args, st.log.data_ptr(), L, 0, MAX_SEQ, SCALE,
-                            torch.cuda.current_stream().cuda_stream)
+def _call(lib, name, st, first, n, stream=None):
+    stream = torch.cuda.current_stream().cuda_stream if stream is None else stream
+    return getattr(lib, name)(first, n, *st.args, st.log.data_ptr(), L, 0, MAX_SEQ, SCALE, stream)
+
+
+def _run(lib, name, w, packed, first, n, st=None):
+    st = State(w, packed, n) if st is None else st
+    rc = _call(lib, name, st, first, n)
     assert rc == 0, f"{name} returned {rc}"
     torch.cuda.synchronize()
     assert lib.qwen_last_error() == 0
@@ -76,7 +83,12 @@ def test_noalloc_matches_generate_nosync_twice():
     ids = qw.synthetic_prompt(2, seed=41)
     cases = [(ids[0], 24), (ids[1], 6)]  # the second call is smaller
     print(f"no-alloc: cases {cases}", flush=True)
-    got = [_run(lib, "qwen_generate_nosync_noalloc", w, packed, f, n) for f, n in cases]
+    states = [State(w, packed, n) for _, n in cases]
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    got = [_run(lib, "qwen_generate_nosync_noalloc", w, packed, f, n, st) for (f, n), st in zip(cases, states)]
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 == free0, f"device free memory changed across the no-allocation calls: {free0} -> {free1}"
     ref = [_run(lib, "launch_ldg_generate_nosync", w, packed, f, n) for f, n in cases]
     for (f, n), a, b in zip(cases, got, ref):
         assert a.log.cpu().tolist() == b.log.cpu().tolist(), (f, n)
@@ -87,3 +99,25 @@ def test_noalloc_matches_generate_nosync_twice():
     again = _run(lib, "qwen_generate_nosync_noalloc", w, packed, *cases[1])
     assert again.log.cpu().tolist() == ref[1].log.cpu().tolist()
     assert torch.equal(again.kc, ref[1].kc)
+
+
+def test_noalloc_refused_under_capture():
+    """A replayed graph would reuse the launch's token epochs: the entry point refuses a capturing
+    stream (QWEN_ERR_ARG = 1) and records nothing into the graph."""
+    import Qwen06B_architecture as qa
+
+    lib = _bind()
+    hw = qw.host_weights(seed=0, std=0.02)
+    w = qw.device_weights(hw, "cuda")
+    packed = qa._pack_layer_weights(w["layer_weights"])
+    st = State(w, packed, 2)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(g, stream=side):
+        rcs.append(_call(lib, "qwen_generate_nosync_noalloc", st, 1, 2, stream=side.cuda_stream))
+    torch.cuda.synchronize()
+    assert rcs == [1]
+    assert st.log.cpu().tolist() == [-1, -1]
+    assert lib.qwen_last_error() == 0
