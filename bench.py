@@ -118,6 +118,47 @@ def aux_line(metric, value, unit, higher, workload, cfg, kernel, bytes_per_call,
     }
 
 
+GOLDEN_C0 = os.path.join(REPO, "tests", "golden", "c0_decode.json")
+
+
+def fixture_agreement(hw, w):
+    """Greedy-token agreement with the committed C0 fixture (tests/golden/c0_decode.json: the
+    16-id prompt, then 32 greedy steps of the fp32 oracle on the same seeded weights), the
+    correctness line the reference's benchmark prints beside its throughput
+    (Model/benchmark.py:128-246, token agreement with HF). Free-running: the engine's 32 greedy
+    tokens after the prompt against the fixture's, up to the fixture's first near-tie step (top-2
+    gap < 1e-2, where either choice meets the parity contract and the two runs may part).
+    Teacher-forced: every step's argmax given the fixture's inputs, near-ties exempt. Uses the
+    fixture file only (no oracle run)."""
+    import numpy as np
+    import torch
+
+    import qwen_megakernel_C
+    import Qwen06B_architecture as qa
+
+    g = json.load(open(GOLDEN_C0))
+    steps = g["steps"]
+    prompt, n = [int(t) for t in g["prompt"]], len(steps)
+    near = [s["gap"] < 1e-2 for s in steps]
+    first_tie = near.index(True) if any(near) else n
+    dec = qa.Decoder(weights=w, verbose=False)
+    dec.prefill(prompt[:-1])
+    free = dec.generate_nosync(prompt[-1], n).cpu().tolist()
+    free_ok = sum(int(free[i] == g["tokens"][i]) for i in range(first_tie))
+    dec.reset()
+    dec._prefill_kv(prompt[:-1])
+    inputs = [int(s["input"]) for s in steps]
+    forced = torch.from_numpy(np.array(inputs, dtype=np.int32)).cuda()
+    t = dec._tensors()
+    out = qwen_megakernel_C.generate_ex(inputs[0], n, forced, *t[:9], dec._norm_out, None, None, 28, len(prompt) - 1,
+                                        qa.MAX_SEQ_LEN, dec._attn_scale).cpu().tolist()
+    qa._check_device_errors()
+    tf_ok = sum(int(out[i] == s["token"]) for i, s in enumerate(steps) if not near[i])
+    return {"fixture": "tests/golden/c0_decode.json", "weights_match": hw.digest() == g["weights_sha256"],
+            "free_running_agree": f"{free_ok}/{first_tie}", "first_near_tie_step": first_tie,
+            "teacher_forced_agree": f"{tf_ok}/{n - sum(near)}", "near_ties_exempt": sum(near)}
+
+
 def run_generate(args, n_prompt, n_new, name):
     """C0 / C3: prefill an n_prompt-id prompt (all but its last id), then one generate_nosync
     launch of n_new greedy tokens; the median launch time over --steps launches."""
@@ -126,7 +167,8 @@ def run_generate(args, n_prompt, n_new, name):
     import qwen_weights as qw
     import Qwen06B_architecture as qa
 
-    w = qw.device_weights(qw.host_weights(seed=0, std=0.02), "cuda")
+    hw = qw.host_weights(seed=0, std=0.02)
+    w = qw.device_weights(hw, "cuda")
     dec = qa.Decoder(weights=w, verbose=False)
     prompt = qw.synthetic_prompt(n_prompt, seed=1)
     ts = []
@@ -144,10 +186,12 @@ def run_generate(args, n_prompt, n_new, name):
     qa._check_device_errors()
     ms = _median(ts)
     start = n_prompt - 1
-    return aux_line(f"batch-1 decode tokens/sec ({name}: {n_prompt}-id prompt, generate_nosync {n_new})",
+    line = aux_line(f"batch-1 decode tokens/sec ({name}: {n_prompt}-id prompt, generate_nosync {n_new})",
                     round(n_new / ms * 1e3, 2), "tokens/s", True, name,
                     {"prompt": n_prompt, "new_tokens": n_new, "positions": f"{start}..{start + n_new - 1}"},
                     "fast::qwen_decode_kernel", algorithmic_bytes(start, n_new), ms, args.steps, args.warmup)
+    line["correctness"] = fixture_agreement(hw, w)
+    return line
 
 
 def run_lm_head(args):
@@ -326,7 +370,8 @@ def run_generate_e2e(args):
     import qwen_weights as qw
     import Qwen06B_architecture as qa
 
-    w = qw.device_weights(qw.host_weights(seed=0, std=0.02), "cuda")
+    hw = qw.host_weights(seed=0, std=0.02)
+    w = qw.device_weights(hw, "cuda")
     dec = qa.Decoder(weights=w, verbose=False)
     n_prompt, n_new = 1000, 1000
     prompt = qw.synthetic_prompt(n_prompt, seed=1)
@@ -352,10 +397,12 @@ def run_generate_e2e(args):
                         "prefill included", round(n_new / ms * 1e3, 2), "tokens/s", True, args.workload, cfg,
                         kernels + " + pf::qwen_prefill_kernel", algorithmic_bytes(n_prompt - 1, n_new), ms,
                         args.steps, args.warmup)
-    return aux_line("Decoder.generate tokens/sec, 1000-id prompt + 1000 new tokens, prefill included",
+    line = aux_line("Decoder.generate tokens/sec, 1000-id prompt + 1000 new tokens, prefill included",
                     round(n_new / ms * 1e3, 2), "tokens/s", True, "generate", cfg,
                     "fast::qwen_decode_kernel + pf::qwen_prefill_kernel",
                     algorithmic_bytes(n_prompt - 1, n_new), ms, args.steps, args.warmup)
+    line["correctness"] = fixture_agreement(hw, w)
+    return line
 
 
 def main():
@@ -496,6 +543,7 @@ def main():
             "kernel_ms": round(avg_kernel_s * 1e3, 3),
         },
         "cpu_baseline": cpu,
+        "correctness": fixture_agreement(hw, w),
     }
     print(json.dumps(line), flush=True)
 

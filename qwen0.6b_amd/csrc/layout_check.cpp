@@ -425,6 +425,68 @@ int main() {
     CHECK(tag_of(1, 0, 0) != 0 && tag_arg(1) != 0, "tags of epoch >= 1 are never 0");
   }
 
+  // ---- prefill LDS tiles: every operand read puts each 16-lane group on distinct bank units ----
+  // (16-byte reads: the 16 units of 16 bytes of a 256-byte window; transposing 8-byte reads: the
+  // 32 units of 8 bytes). The permutations are also bijections, so the LDS-DMA lane that writes
+  // position p of a row (source chunk perm(p, r)) fills every chunk of the row exactly once.
+  {
+    auto distinct = [](const int* u, int n) {
+      for (int a = 0; a < n; ++a)
+        for (int b = a + 1; b < n; ++b)
+          if (u[a] == u[b]) return false;
+      return true;
+    };
+    // GEMM ring: tile rows of 128 bytes; a read takes rows base + (lane % 16) (base a multiple
+    // of 16) and logical chunk c = 4 ks + lane / 16 at position c ^ pf_swz8(row)
+    for (int base = 0; base < 128; base += 16)
+      for (int ks = 0; ks < 2; ++ks)
+        for (int g = 0; g < 4; ++g) {
+          int u[16], un[16];
+          for (int fr = 0; fr < 16; ++fr) {
+            const int row = base + fr, c = 4 * ks + g;
+            u[fr] = ((row * 128 + 16 * (c ^ pf_swz8(row))) / 16) % 16;
+            un[fr] = ((row * 128 + 16 * c) / 16) % 16;
+          }
+          CHECK(distinct(u, 16), "gemm operand read: bank units repeat (base %d ks %d group %d)", base, ks, g);
+          CHECK(!distinct(un, 16), "the natural chunk order would not conflict (the check would be vacuous)");
+        }
+    for (int r = 0; r < 16; ++r) {
+      int p8[8], pk[16], pv[16];
+      for (int q = 0; q < 8; ++q) p8[q] = q ^ pf_swz8(r);
+      for (int q = 0; q < 16; ++q) {
+        pk[q] = pf_kpos(q, r);
+        pv[q] = pf_vpos(q, r);
+        CHECK(pf_kpos(pk[q], r) == q && pf_vpos(pv[q], r) == q, "K/V chunk permutations are involutions");
+      }
+      CHECK(distinct(p8, 8) && distinct(pk, 16) && distinct(pv, 16), "chunk permutations are bijections (row %d)", r);
+    }
+    // attention K: key rows of 256 bytes; a read takes key rows 16 j + (lane % 16), logical chunk
+    // 4 kk + lane / 16
+    for (int j = 0; j < 4; ++j)
+      for (int kk = 0; kk < 4; ++kk)
+        for (int g = 0; g < 4; ++g) {
+          int u[16];
+          for (int fr = 0; fr < 16; ++fr) u[fr] = pf_kpos(4 * kk + g, 16 * j + fr) % 16;
+          CHECK(distinct(u, 16), "attention K read: bank units repeat (j %d kk %d group %d)", j, kk, g);
+        }
+    // attention V^T by transposing 8-byte reads: lane i of 16-lane group fg addresses key row
+    // kr + i / 4 (kr = 32 kk + 4 fg, + 16), bytes 16 ch + 8 (i % 2) with ch = pf_vpos(2 tt + (i % 4) / 2, row)
+    for (int kk = 0; kk < 2; ++kk)
+      for (int half = 0; half < 2; ++half)
+        for (int fg = 0; fg < 4; ++fg)
+          for (int tt = 0; tt < 8; ++tt) {
+            int u[16], un[16];
+            for (int i = 0; i < 16; ++i) {
+              const int te = i >> 2, tq = i & 3, r = 32 * kk + 16 * half + 4 * fg + te;
+              const int ch = pf_vpos(2 * tt + (tq >> 1), r);
+              u[i] = ((r * 256 + 16 * ch + 8 * (tq & 1)) / 8) % 32;
+              un[i] = ((r * 256 + 16 * (2 * tt + (tq >> 1)) + 8 * (tq & 1)) / 8) % 32;
+            }
+            CHECK(distinct(u, 16), "attention V^T read: bank units repeat (kk %d fg %d tt %d)", kk, fg, tt);
+            CHECK(!distinct(un, 16), "V^T natural order would not conflict (the check would be vacuous)");
+          }
+  }
+
   // ---- 64-bit pointers through the 32-bit lane broadcast (readfirstlane: int -> int) ----
   // Device addresses whose low word has bit 31 set are where a signed broadcast result,
   // widened straight to 64 bits, would corrupt the high word; every such case is checked

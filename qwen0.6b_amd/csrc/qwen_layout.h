@@ -282,6 +282,21 @@ QL_HD unsigned tag_arg(unsigned epoch) { return (epoch << 8) | 255u; }
 QL_HD unsigned tag_logit(unsigned epoch) { return (epoch << 8) | 254u; }
 QL_HD unsigned tag_sel(unsigned epoch) { return (epoch << 8) | 253u; }
 
+// ---- prefill LDS layouts -------------------------------------------------------------
+// The prefill kernel's LDS operand tiles hold each row as 16-byte chunks in a permuted order,
+// so that the rows one MFMA operand read takes fall on distinct banks. Measured on MI355X
+// (each pattern alone, 8 waves per CU): a 16-byte read whose 16-lane groups each touch 16
+// distinct 16-byte bank units of a 256-byte window runs conflict-free; the same reads with the
+// chunks in natural order run 3.5x (GEMM rows of 128 bytes) and, for the transposing 8-byte
+// reads of V, 4.45x slower. layout_check verifies that property for these permutations.
+// GEMM ring rows (128 bytes, 8 chunks): logical chunk q of tile row r at position q ^ pf_swz8(r)
+QL_HD int pf_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+// attention key rows (256 bytes, 16 chunks): chunk q of key row r at position pf_kpos(q, r) for
+// K, pf_vpos(q, r) for V (each its own inverse: the DMA lane at position p loads source chunk
+// pf_kpos(p, r))
+QL_HD int pf_kpos(int q, int r) { return q ^ (r & 15); }
+QL_HD int pf_vpos(int q, int r) { return q ^ (2 * (r & 7)); }
+
 // ---- 64-bit values through a 32-bit lane broadcast -----------------------------------
 // `bcast` stands for the GPU's readfirstlane, which takes and returns a signed int. Each
 // half of v is broadcast on its own and read back through unsigned, so a low half with
