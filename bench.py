@@ -376,7 +376,8 @@ def run_generate_e2e(args):
     n_prompt, n_new = 1000, 1000
     prompt = qw.synthetic_prompt(n_prompt, seed=1)
     sampling = {"sampled": dict(temperature=0.8, top_k=50, top_p=0.95, seed=7),
-                "sampled_t": dict(temperature=0.8, seed=7)}.get(args.workload, {})
+                "sampled_t": dict(temperature=0.8, seed=7),
+                "sampled_p": dict(temperature=0.8, top_p=0.95, seed=7)}.get(args.workload, {})
     ts = []
     for rep in range(args.warmup + args.steps):
         torch.cuda.synchronize()
@@ -390,9 +391,11 @@ def run_generate_e2e(args):
     cfg = {"prompt": n_prompt, "new_tokens": n_new, "positions": f"0..{n_prompt + n_new - 2}"}
     if sampling:
         cfg.update(sampling)
-        what = ("temperature 0.8, top-k 50, top-p 0.95" if "top_k" in sampling else "temperature 0.8")
-        # drawn inside the decode kernel: its top-k build, or its temperature-only build
-        kernels = "sampled::qwen_decode_kernel" if "top_k" in sampling else "tsampled::qwen_decode_kernel"
+        # drawn inside the decode kernel: its top-k build, its split-capable build (top-p alone) or
+        # its temperature-only build
+        what, kernels = {"sampled": ("temperature 0.8, top-k 50, top-p 0.95", "sampled::qwen_decode_kernel"),
+                         "sampled_p": ("temperature 0.8, top-p 0.95", "dsampled::qwen_decode_kernel"),
+                         "sampled_t": ("temperature 0.8", "tsampled::qwen_decode_kernel")}[args.workload]
         return aux_line(f"Decoder.generate tokens/sec with sampling ({what}), 1000-id prompt + 1000 new tokens, "
                         "prefill included", round(n_new / ms * 1e3, 2), "tokens/s", True, args.workload, cfg,
                         kernels + " + pf::qwen_prefill_kernel", algorithmic_bytes(n_prompt - 1, n_new), ms,
@@ -418,12 +421,13 @@ def main():
                     help="after timing, record per-stage device timestamps of token 64 of one more step "
                          "into this .npy file ([256 workgroups, 8 x 28 + 1 stages, events], 100 MHz ticks)")
     ap.add_argument("--workload", default="c4",
-                    choices=["c4", "c3", "c0", "c1", "c2", "prefill", "generate", "sampled", "sampled_t"],
+                    choices=["c4", "c3", "c0", "c1", "c2", "prefill", "generate", "sampled", "sampled_t",
+                             "sampled_p"],
                     help="c4 (default): the headline decode at context 1921..2048; c3: 128-id prompt + "
                          "generate_nosync 512; c0: 16 + 32; c1: isolated lm_head + argmax; c2: isolated MLP block; "
                          "prefill: batched prefill of 1920 ids; generate: Decoder.generate_ids 1000 + 1000 "
                          "with its prefill; sampled: the same with temperature 0.8, top-k 50, top-p 0.95; "
-                         "sampled_t: with temperature 0.8 alone")
+                         "sampled_t: with temperature 0.8 alone; sampled_p: with temperature 0.8, top-p 0.95")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine runs one sequence on one MI355X; --gpus {args.gpus} "
@@ -434,7 +438,8 @@ def main():
         runs = {"c3": lambda: run_generate(args, 128, 512, "c3"), "c0": lambda: run_generate(args, 16, 32, "c0"),
                 "c1": lambda: run_lm_head(args), "c2": lambda: run_mlp(args),
                 "prefill": lambda: run_prefill(args), "generate": lambda: run_generate_e2e(args),
-                "sampled": lambda: run_generate_e2e(args), "sampled_t": lambda: run_generate_e2e(args)}
+                "sampled": lambda: run_generate_e2e(args), "sampled_t": lambda: run_generate_e2e(args),
+                "sampled_p": lambda: run_generate_e2e(args)}
         print(json.dumps(runs[args.workload]()), flush=True)
         return
 

@@ -198,21 +198,20 @@ int qwen_sample(const float* logits, int n, float temperature, int top_k, float 
                 unsigned long long seed, unsigned int step, int* out_token, hipStream_t stream);
 
 /* Sampled generation (no counterpart in the reference): generate_nosync whose
- * every next token comes from qwen_sample over that step's logits (seed,
- * step = the position of the step's input token) instead of the argmax. With
- * temperature > 0 and either top_k 0 (or >= 151936) and top_p >= 1 (temperature
- * alone), or 1 <= top_k <= 128 (any top_p), the decode kernel's sampling build
- * draws each token itself in one launch of num_steps steps (the same kept set
- * and draw as qwen_sample); otherwise it runs as num_steps pairs of launches (a
- * decode step, then the sampler); neither synchronises with the host. With eos_token_id >= 0 the generation ends after the
- * first sampled eos: output_log[0 .. n) holds the sampled ids, eos last when it
- * was reached, later entries are -1, and n = *out_count (device int32,
- * nullable) <= num_steps; the K/V cache holds positions start_position ..
- * start_position + n - 1. In the pairs-of-launches form the launches after
- * the eos still run (the host enqueued them) and their results mean nothing:
- * K/V entries past that range, hidden_buffer and g_normalized; a caller that
- * expects an early eos enqueues shorter runs. That form allocates a 759 KB
- * per-device buffer on first use. */
+ * every next token is drawn as qwen_sample draws it from that step's logits
+ * (seed, step = the position of the step's input token) instead of the argmax.
+ * Every parameter set runs as one launch of num_steps steps in which the decode
+ * kernel draws each token itself (the same kept set and draw as qwen_sample):
+ * temperature <= 0 or top_k == 1 is the argmax; temperature alone, top-k with
+ * 1 <= top_k <= 128 (any top_p), and top-p alone or a larger top_k each have a
+ * build of the kernel of their own. The last form decides from the 8 largest
+ * logits of each of 256 vocabulary slices when those suffice and otherwise
+ * splits its radix selections over every workgroup's slice. No host
+ * synchronisation. With eos_token_id >= 0 the generation ends on the device
+ * after the first sampled eos: output_log[0 .. n) holds the sampled ids, eos
+ * last when it was reached, later entries are -1, and n = *out_count (device
+ * int32, nullable) <= num_steps; the K/V cache holds positions start_position ..
+ * start_position + n - 1. */
 int qwen_generate_sampled(
     int first_token_id, int num_steps, int eos_token_id, const void* embed_weight,
     const LDGLayerWeight* layer_weights, const void* final_norm_weight,
@@ -228,11 +227,11 @@ int qwen_generate_sampled(
 int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token,
                         float* logits_out, hipStream_t stream);
 
-/* Isolated lm_head + top-k draw (no counterpart in the reference): the same
- * logits as qwen_lm_head_argmax, then the token the decode kernel's sampling
- * build draws inside a top-k generation (temperature > 0, 1 <= top_k <= 128,
- * top_p as in qwen_sample; Philox step = position). It equals qwen_sample on
- * logits_out with the same arguments; it exists to test that in-kernel draw. */
+/* Isolated lm_head + draw (no counterpart in the reference): the same logits
+ * as qwen_lm_head_argmax, then the token the decode kernel's sampling builds
+ * draw inside a sampled generation (temperature > 0, top_k >= 0 and top_p as in
+ * qwen_sample; Philox step = position). It equals qwen_sample on logits_out
+ * with the same arguments; it exists to test those in-kernel draws. */
 int qwen_lm_head_sample(const void* hidden_f16, const void* weight, float temperature, int top_k,
                         float top_p, unsigned long long seed, int position, int* out_token,
                         float* logits_out, hipStream_t stream);

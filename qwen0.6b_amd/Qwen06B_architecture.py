@@ -49,11 +49,6 @@ DEVICE = "cuda"  # where Decoder allocates its state; the engine itself needs th
 _OPS = ("decode", "generate_nosync", "generate_until")
 
 
-# sampled generation with an eos id: steps enqueued between two host checks for the eos
-SAMPLED_CHUNK = 32
-# largest top_k the decode kernel draws from itself (a sampled generation is then one launch)
-TOPK_IN_KERNEL = 128
-
 
 def _require_megakernel_op(op_name: str):
     """Return an op from the extension module or the torch.ops namespace."""
@@ -375,42 +370,27 @@ class Decoder:
 
     def generate_sampled(self, first_token_id: int, max_tokens: int, temperature: float, top_k: int = 0,
                          top_p: float = 1.0, seed: int = 0, eos_token_id=None) -> list:
-        """Up to ``max_tokens`` sampled steps from the current position, with no host
-        synchronisation until the end: each step's next token is drawn on the device from
-        its logits (temperature, then top-k, then top-p, then a draw seeded by ``seed`` and
-        the step's position; temperature <= 0 or top_k == 1 is greedy). With
-        ``eos_token_id`` the generation ends after that id (which ends the list): on the
-        device when the decode kernel draws the tokens itself (temperature alone, or
-        1 <= top_k <= ``TOPK_IN_KERNEL``), else checked on the host every ``SAMPLED_CHUNK``
-        steps (the steps enqueued after an eos are wasted work); advances the position by
-        the number of steps run."""
+        """Up to ``max_tokens`` sampled steps from the current position in one launch of the
+        decode kernel, with no host synchronisation until the end: each step's next token is
+        drawn on the device from its logits (temperature, then top-k, then top-p, then a draw
+        seeded by ``seed`` and the step's position; temperature <= 0 or top_k == 1 is greedy).
+        With ``eos_token_id`` the device ends the generation after that id (which ends the
+        list); advances the position by the number of steps run."""
         if self._position + max_tokens > MAX_SEQ_LEN:
             raise RuntimeError(f"positions {self._position}..{self._position + max_tokens} exceed {MAX_SEQ_LEN}")
         if top_k < 0 or not 0.0 <= top_p or temperature != temperature:
             raise ValueError(f"invalid sampling parameters temperature={temperature} top_k={top_k} top_p={top_p}")
         gen = _require_megakernel_op("generate_sampled")
         eos = -1 if eos_token_id is None else int(eos_token_id)
-        # temperature alone, and top-k up to TOPK_IN_KERNEL, run as one launch that checks eos
-        # on the device: no chunking
-        one_launch = temperature > 0 and (((top_k == 0 or top_k >= VOCAB_SIZE) and top_p >= 1.0)
-                                          or 1 <= top_k <= TOPK_IN_KERNEL)
-        chunk = max_tokens if eos < 0 or one_launch else SAMPLED_CHUNK
-        out, first = [], int(first_token_id)
-        while len(out) < max_tokens:
-            m = min(chunk, max_tokens - len(out))
-            ids, count = gen(first, m, eos, self._embed_weight, self._layer_weights_packed, self._final_norm_weight,
-                             self._lm_head_weight, self._cos_table, self._sin_table, self._k_cache, self._v_cache,
-                             self._hidden, self._norm_out, self._num_layers, self._position, MAX_SEQ_LEN,
-                             self._attn_scale, float(temperature), int(top_k), float(top_p),
-                             int(seed) & 0xFFFFFFFFFFFFFFFF)
-            n = int(count.item())
-            _check_device_errors()
-            self._position += n
-            out += ids[:n].cpu().tolist()
-            if n < m or out[-1] == eos:
-                break
-            first = out[-1]
-        return out
+        ids, count = gen(int(first_token_id), max_tokens, eos, self._embed_weight, self._layer_weights_packed,
+                         self._final_norm_weight, self._lm_head_weight, self._cos_table, self._sin_table,
+                         self._k_cache, self._v_cache, self._hidden, self._norm_out, self._num_layers, self._position,
+                         MAX_SEQ_LEN, self._attn_scale, float(temperature), int(top_k), float(top_p),
+                         int(seed) & 0xFFFFFFFFFFFFFFFF)
+        n = int(count.item())
+        _check_device_errors()
+        self._position += n
+        return ids[:n].cpu().tolist()
 
     def generate_ids(self, ids, max_tokens: int = 100, eos_token_id=None, temperature: float = 0.0,
                      top_k: int = 0, top_p: float = 1.0, seed: int = 0) -> list:

@@ -38,7 +38,13 @@ int main() {
   CHECK(XCD_SLOTS % 2 == 0 && OFF_ARG % 2 == 0, "xcd / arg alignment");
   CHECK(xbuf(1, NXCD - 1, XCD_SLOTS) == OFF_ARG, "xcd buffers end at the ARG buffer");
   CHECK(OFF_ARG + 2L * ARG_SLOTS == OFF_LOGIT && OFF_LOGIT + LOGIT_SLOTS == OFF_SEL &&
-            OFF_SEL + SEL_SLOTS == TOTAL_SLOTS, "ARG, LOGIT, SEL end");
+            OFF_SEL + SEL_SLOTS == OFF_DIST && OFF_DIST + DIST_SLOTS == TOTAL_SLOTS, "ARG, LOGIT, SEL, DIST end");
+  CHECK(OFF_DIST % 2 == 0, "DIST pairs are 16-byte aligned");
+  // DIST tags sit between the stage tags and the LOGIT / SEL / ARG tags of the same epoch
+  CHECK((tag_of(1, MAX_LAYERS - 1, NSTAGE - 1) & 255u) < (tag_dist(1, 0) & 255u) &&
+            (tag_dist(1, DIST_ROUNDS - 1) & 255u) < (tag_sel(1) & 255u), "DIST tags are distinct");
+  CHECK(dhist_off(1, DHIST_PASSES - 1) + 256 * 8 == 256 + LM_CTR_BYTES + DHIST_BYTES &&
+            TOTAL_SLOTS * 8 + dhist_off(0, 0) + DHIST_BYTES == WORKSPACE_BYTES, "DHIST ends the workspace");
   CHECK(OFF_LOGIT % 2 == 0 && LOGIT_SLOTS % 2 == 0 && OFF_SEL % 2 == 0, "LOGIT / SEL pairs are 16-byte aligned");
   CHECK(OFF_LOGIT % LM_CHUNK == 0 && slot_logit(0) == OFF_LOGIT && slot_logit(VOCAB - 1) == OFF_LOGIT + VOCAB - 1,
         "an lm_head chunk's logits are one 64-byte line");
@@ -51,7 +57,7 @@ int main() {
     }
     CHECK(used == VOCAB, "slice sizes sum to the vocabulary");
   }
-  CHECK(TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
+  CHECK(TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES + DHIST_BYTES == WORKSPACE_BYTES && WORKSPACE_BYTES < (1L << 31), "workspace size");
   CHECK(BLOCK == 512 && NLOC == 32 && NXCD * NLOC == NWG, "grid constants");
   for (int w = 0; w < NWG; ++w) CHECK(8 * loc_of(w) + xcd_of(w) == w, "w = 8 i + x");
 

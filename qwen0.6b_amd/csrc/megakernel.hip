@@ -110,12 +110,14 @@ struct KParams {
   float temperature;
   u64 seed;
   int sample;              // host side: launch the sampling build
-  // the sampling build with 1 <= top_k <= TOPK_MAX: the token is drawn from the top-k (then
-  // top-p, when top_p < 1) tokens of the step's logits (draw_topk) instead of from all of them
+  // the sampling builds with top_k >= 1: the token is drawn from the top-k (then top-p, when
+  // top_p < 1) tokens of the step's logits instead of from all of them; top_k = VOCAB: top-p
+  // alone. 1 <= top_k <= TOPK_MAX: the `sampled` build (draw_topk); larger: `dsampled`
+  // (draw_dist); top_k = 0: `tsampled` (temperature alone)
   int top_k;
   float top_p;
 };
-constexpr int TOPK_MAX = 128;  // largest top_k the decode kernel draws from itself
+constexpr int TOPK_MAX = 128;  // largest top_k of the `sampled` build
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): 10 rounds of two 32x32 -> 64 multiplies
 // with the published multipliers and key increments; returns the first output word
@@ -172,6 +174,7 @@ namespace fast {
 constexpr bool kTrace = false;
 constexpr bool kSample = false;
 constexpr bool kTopK = false;
+constexpr bool kDist = false;
 #include "decode_body.inc"
 }  // namespace fast
 
@@ -179,6 +182,7 @@ namespace traced {
 constexpr bool kTrace = true;
 constexpr bool kSample = false;
 constexpr bool kTopK = false;
+constexpr bool kDist = false;
 #include "decode_body.inc"
 }  // namespace traced
 
@@ -186,8 +190,19 @@ namespace sampled {
 constexpr bool kTrace = false;
 constexpr bool kSample = true;
 constexpr bool kTopK = true;
+constexpr bool kDist = false;
 #include "decode_body.inc"
 }  // namespace sampled
+
+// top_k > TOPK_MAX and top-p alone: the sampling build whose draw splits the selections over
+// every workgroup's slice when the published entries cannot decide them (draw_dist)
+namespace dsampled {
+constexpr bool kTrace = false;
+constexpr bool kSample = true;
+constexpr bool kTopK = true;
+constexpr bool kDist = true;
+#include "decode_body.inc"
+}  // namespace dsampled
 
 // temperature alone: the sampling build without the top-k draw, whose code would otherwise
 // share (and reshape) this kernel's register allocation
@@ -195,6 +210,7 @@ namespace tsampled {
 constexpr bool kTrace = false;
 constexpr bool kSample = true;
 constexpr bool kTopK = false;
+constexpr bool kDist = false;
 #include "decode_body.inc"
 }  // namespace tsampled
 
@@ -248,7 +264,7 @@ struct DeviceState {
   Workspace fixed;                // the `scratch` array of this device (no allocation)
   LDGLayerWeight* tab = nullptr;  // the isolated MLP block's one-layer pointer table
   char* pf = nullptr;             // prefill activations (PF_BYTES), on first use
-  char* smp = nullptr;            // sampler work area, sampled generation's step buffers (SMP_BYTES)
+  char* smp = nullptr;            // the sampler's work area (SMP_BYTES), allocated on first use
   u32 smp_parity = 0;             // sampler launches so far (selects the work area copy)
   u64 clk_khz = 100000;
   u64 deadline = 0;
@@ -380,8 +396,9 @@ int launch(KParams& P, hipStream_t stream, bool fixed = false) {
   w.epoch = (u32)next;
   void* args[] = {&P};
   const void* kernel = P.trace    ? (const void*)traced::qwen_decode_kernel
-                       : P.sample ? (P.top_k > 0 ? (const void*)sampled::qwen_decode_kernel
-                                                 : (const void*)tsampled::qwen_decode_kernel)
+                       : P.sample ? (P.top_k > TOPK_MAX ? (const void*)dsampled::qwen_decode_kernel
+                                    : P.top_k > 0      ? (const void*)sampled::qwen_decode_kernel
+                                                       : (const void*)tsampled::qwen_decode_kernel)
                                   : (const void*)fast::qwen_decode_kernel;
   if (hipLaunchCooperativeKernel(kernel, dim3(NWG), dim3(BLOCK), args, 0, stream) != hipSuccess)
     return QWEN_ERR_LAUNCH;
@@ -444,21 +461,24 @@ static int prefill_units(int n, int start, pf::PParams& P) {
   return QWEN_OK;
 }
 
-// sampler buffer: the sampler's work area, one step's fp32 logits, the step's greedy id (unused),
-// the sampled id, and the embedding row of the sampled id (the next decode step's one-row
-// embedding table)
+// sampler buffer: the sampler's work area (two copies, chosen by launch parity)
 constexpr long SMP_WORK = 0;
-constexpr long SMP_LOGITS = SMP_WORK + (smp::WORK_BYTES + 255) / 256 * 256;
-constexpr long SMP_ARGMAX = SMP_LOGITS + (long)VOCAB * 4;
-constexpr long SMP_TOKEN = SMP_ARGMAX + 256;
-constexpr long SMP_ROW = SMP_TOKEN + 256;
-constexpr long SMP_BYTES = SMP_ROW + HIDDEN * 2;
+constexpr long SMP_BYTES = (smp::WORK_BYTES + 255) / 256 * 256;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 // temperature, top_k and top_p as the sampler reads them (NaN refused)
 bool sample_args_ok(float temperature, int top_k, float top_p) {
   return temperature == temperature && top_k >= 0 && top_p == top_p;
+}
+
+// the decode kernel's top_k for a draw with these arguments (checked by sample_args_ok):
+// temperature <= 0 is the argmax (1); no top-k (0 or >= VOCAB) is VOCAB with top_p < 1 (top-p
+// alone) and 0 without (temperature alone)
+int device_top_k(float temperature, int top_k, float top_p) {
+  if (!(temperature > 0.f)) return 1;
+  if (top_k == 0 || top_k >= VOCAB) return top_p < 1.f ? VOCAB : 0;
+  return top_k;
 }
 
 // the device's sampler buffer (allocated and cleared on first use); caller holds g_mu
@@ -737,7 +757,6 @@ extern "C" int qwen_sample(const float* logits, int n, float temperature, int to
   S.seed = seed;
   S.step = step;
   S.out_token = out_token;
-  S.eos = -1;
   return launch_sampler(st, S, stream);
 }
 
@@ -757,63 +776,20 @@ extern "C" int qwen_generate_sampled(int first_token_id, int num_steps, int eos_
   if (!output_log || first_token_id < 0 || first_token_id >= VOCAB || eos_token_id < -1 || eos_token_id >= VOCAB ||
       !sample_args_ok(temperature, top_k, top_p))
     return QWEN_ERR_ARG;
-  const bool fused_k = temperature > 0.f && top_k >= 1 && top_k <= TOPK_MAX;
-  if (fused_k || (temperature > 0.f && (top_k == 0 || top_k >= VOCAB) && !(top_p < 1.f))) {
-    // temperature alone, or top-k with top_k <= TOPK_MAX: the decode kernel's sampling build
-    // draws every token itself (one launch, eos checked on the device as in qwen_generate_until)
-    P.first_token = first_token_id;
-    P.out_tokens = output_log;
-    P.out_count = out_count;
-    P.eos = eos_token_id;
-    P.temperature = temperature;
-    P.seed = seed;
-    P.sample = 1;
-    P.top_k = fused_k ? top_k : 0;
-    P.top_p = top_p;
-    return launch(P, stream);
-  }
-  char* buf = nullptr;
-  DeviceState* st = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    if ((rc = device_state(&st)) != QWEN_OK || (rc = sampler_buffer(st, stream)) != QWEN_OK) return rc;
-    buf = st->smp;
-  }
-  float* logits = (float*)(buf + SMP_LOGITS);
-  int* tok = (int*)(buf + SMP_TOKEN);
-  _Float16* row = (_Float16*)(buf + SMP_ROW);
-  smp::SParams S;
-  memset(&S, 0, sizeof(S));
-  S.logits = logits;
-  S.n = VOCAB;
-  S.temperature = temperature;
-  S.top_k = top_k;
-  S.top_p = top_p;
-  S.seed = seed;
-  S.out_token = tok;
-  S.eos = eos_token_id;
-  S.out_count = out_count;
-  S.embed = (const _Float16*)embed_weight;
-  S.row = row;
-  // Per step: one decode launch writing the step's logits, then the sampler. The host never
-  // waits, so the decode step cannot take its input id as an argument: from step 1 on its
-  // embedding table is the one row the sampler copied out for the id it drew (input id 0).
-  for (int s = 0; s < num_steps; ++s) {
-    if ((rc = fill_decode(P, s == 0 ? embed_weight : (const void*)row, layer_weights, final_norm_weight,
-                          lm_head_weight, cos_table, sin_table, k_cache, v_cache, hidden_buffer, g_normalized,
-                          num_layers, start_position + s, 1, max_seq_len, attn_scale)) != QWEN_OK)
-      return rc;
-    P.first_token = s == 0 ? first_token_id : 0;
-    P.out_tokens = (int*)(buf + SMP_ARGMAX);
-    P.logits_out = logits;
-    if ((rc = launch(P, stream)) != QWEN_OK) return rc;
-    S.step = (u32)(start_position + s);
-    S.out_log = output_log + s;
-    S.index = s;
-    std::lock_guard<std::mutex> lock(g_mu);
-    if ((rc = launch_sampler(st, S, stream)) != QWEN_OK) return rc;
-  }
-  return QWEN_OK;
+  // one launch of num_steps steps, every token drawn inside the decode kernel (eos checked on the
+  // device as in qwen_generate_until): temperature <= 0 is the argmax (top_k 1); temperature
+  // alone runs the `tsampled` build, top-k (then top-p) and top-p alone the `sampled` /
+  // `dsampled` builds
+  P.first_token = first_token_id;
+  P.out_tokens = output_log;
+  P.out_count = out_count;
+  P.eos = eos_token_id;
+  P.temperature = temperature;
+  P.seed = seed;
+  P.sample = 1;
+  P.top_k = device_top_k(temperature, top_k, top_p);
+  P.top_p = top_p;
+  return launch(P, stream);
 }
 
 extern "C" int qwen_lm_head_argmax(const void* hidden_f16, const void* weight, int* out_token, float* logits_out,
@@ -839,7 +815,7 @@ extern "C" int qwen_lm_head_sample(const void* hidden_f16, const void* weight, f
                                    float* logits_out, hipStream_t stream) {
   if (!hidden_f16 || !weight || !out_token || !aligned16(hidden_f16) || !aligned16(weight)) return QWEN_ERR_ARG;
   if (logits_out && !aligned16(logits_out)) return QWEN_ERR_ARG;
-  if (!(temperature > 0.f) || top_k < 1 || top_k > TOPK_MAX || top_p != top_p || position < 0) return QWEN_ERR_ARG;
+  if (!(temperature > 0.f) || !sample_args_ok(temperature, top_k, top_p) || position < 0) return QWEN_ERR_ARG;
   KParams P;
   memset(&P, 0, sizeof(P));
   P.eos = -1;
@@ -855,7 +831,7 @@ extern "C" int qwen_lm_head_sample(const void* hidden_f16, const void* weight, f
   P.temperature = temperature;
   P.seed = seed;
   P.sample = 1;
-  P.top_k = top_k;
+  P.top_k = device_top_k(temperature, top_k, top_p);
   P.top_p = top_p;
   return launch(P, stream);
 }

@@ -260,9 +260,26 @@ constexpr long OFF_LOGIT = OFF_ARG + 2L * ARG_SLOTS;
 constexpr long LOGIT_SLOTS = VOCAB;
 constexpr long OFF_SEL = OFF_LOGIT + LOGIT_SLOTS;
 constexpr long SEL_SLOTS = 2L * NWG * SEL_DEPTH;   // 4096
-constexpr long TOTAL_SLOTS = OFF_SEL + SEL_SLOTS;
-// after the slots: one 256-byte line of status words, then the lm_head pool counters
-constexpr long WORKSPACE_BYTES = TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES;
+// Draws split by slice (the build for top_k > TOPK_MAX and for top-p alone): every workgroup
+// adds its slice's radix histogram into a global one (DHIST) with device-scope atomics, then
+// announces it in a DIST round: one slot pair per workgroup per round, tagged
+// tag_dist(epoch, round). Rounds also carry each slice's mass sum and Gumbel maximum, so
+// every round has its own slots (a slow workgroup never finds a later round's tag in place
+// of the one it waits for).
+constexpr int DIST_ROUNDS = 10;  // 4 count passes, the mass total, 4 mass passes, the draw
+constexpr long OFF_DIST = OFF_SEL + SEL_SLOTS;
+constexpr long DIST_SLOTS = 2L * NWG * DIST_ROUNDS;  // 5120
+constexpr long TOTAL_SLOTS = OFF_DIST + DIST_SLOTS;
+// DHIST: per token parity, 8 passes x 256 bins of u64 (workgroup 0 clears the token's copy as
+// the token starts: the token two back, which used it, has ended in every workgroup)
+constexpr int DHIST_PASSES = 8;
+constexpr long DHIST_BYTES = 2L * DHIST_PASSES * 256 * 8;
+// after the slots: one 256-byte line of status words, the lm_head pool counters, DHIST
+constexpr long WORKSPACE_BYTES = TOTAL_SLOTS * 8 + 256 + LM_CTR_BYTES + DHIST_BYTES;
+// byte offset of DHIST pass `pass` of token `epoch` from the status line
+QL_HD long dhist_off(unsigned epoch, int pass) {
+  return 256 + LM_CTR_BYTES + ((long)(epoch & 1u) * DHIST_PASSES + pass) * 256 * 8;
+}
 
 // first slot of buffer `b` (one of B_*) of XCD x, parity par
 QL_HD long xbuf(int par, int x, long b) { return ((long)par * NXCD + x) * XCD_SLOTS + b; }
@@ -281,6 +298,7 @@ QL_HD unsigned tag_of(unsigned epoch, int layer, int st) { return (epoch << 8) |
 QL_HD unsigned tag_arg(unsigned epoch) { return (epoch << 8) | 255u; }
 QL_HD unsigned tag_logit(unsigned epoch) { return (epoch << 8) | 254u; }
 QL_HD unsigned tag_sel(unsigned epoch) { return (epoch << 8) | 253u; }
+QL_HD unsigned tag_dist(unsigned epoch, int round) { return (epoch << 8) | (unsigned)(232 + round); }
 
 // ---- prefill LDS layouts -------------------------------------------------------------
 // The prefill kernel's LDS operand tiles hold each row as 16-byte chunks in a permuted order,

@@ -286,7 +286,8 @@ torch::Tensor lm_head_sample(torch::Tensor hidden, torch::Tensor weight, double 
     check_dev(*logits_out, "logits_out", torch::kFloat, V);
     lo = logits_out->data_ptr<float>();
   }
-  TORCH_CHECK(top_k >= 1 && top_k <= 128 && position >= 0 && position < (1LL << 31), "lm_head_sample: top_k in [1, 128]");
+  TORCH_CHECK(temperature > 0 && top_k >= 0 && position >= 0 && position < (1LL << 31),
+              "lm_head_sample: temperature > 0, top_k >= 0, position >= 0");
   auto out = torch::zeros({1}, torch::dtype(torch::kInt32).device(weight.device()));
   check_rc(qwen_lm_head_sample(hidden.data_ptr(), weight.data_ptr(), (float)temperature, (int)top_k, (float)top_p, seed,
                                (int)position, out.data_ptr<int>(), lo, stream_of(weight)),

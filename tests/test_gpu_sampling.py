@@ -220,9 +220,67 @@ def test_in_kernel_topk_draw_matches_oracle(ext, lm_e0, kind):
 
 def test_in_kernel_topk_draw_errors(ext, lm_e0):
     w, h = lm_e0
-    for t, k in [(0.0, 5), (1.0, 0), (1.0, 129)]:
+    for t, k, p in [(0.0, 5, 1.0), (-1.0, 0, 0.9), (1.0, -1, 1.0), (1.0, 5, float("nan"))]:
         with pytest.raises(RuntimeError):
-            ext.lm_head_sample(h, w, t, k, 1.0, 1, 0)
+            ext.lm_head_sample(h, w, t, k, p, 1, 0)
+
+
+def _u_decides(x, temperature, top_k, top_p):
+    """Whether the split-capable draw (top-p alone, top_k > 128) decides from the slices'
+    published entries U: a top-k of at most 2048 whose k-th largest key of U is above every
+    slice's 8th largest key, or a top-p cut (no top-k) above every slice's 8th largest key;
+    otherwise it splits the selections over every slice."""
+    keys = sp.fkey(x).astype(np.int64)
+    rows = np.arange(V)
+    published, last = [], []
+    for w in range(256):
+        idx = rows[w::256]
+        top = idx[np.lexsort((idx, -keys[idx]))[:8]]
+        published.extend(keys[top])
+        last.append(keys[top[7]])
+    if 0 < top_k < V:
+        if top_k > 8 * 256:
+            return False
+        return max(last) < np.sort(np.array(published))[::-1][top_k - 1]
+    _, info = sp.kept_set(x, temperature, 0, top_p)
+    return max(last) < info["lo"]
+
+
+@pytest.mark.parametrize("kind", ["normal", "cluster", "flat", "grid", "special", "inf"])
+def test_in_kernel_split_draw_matches_oracle(ext, lm_e0, kind):
+    """The decode kernel's draw for top-p alone and for top_k > 128 (decided from the slices'
+    published entries when they can, else by radix passes over every workgroup's slice with a
+    global histogram per pass) picks the oracle's token on the same logits, up to the same
+    exemptions as the sampler kernel; "normal", "grid" and "special" take both paths here,
+    "cluster" and "flat" the split one."""
+    w, h = lm_e0
+    rng = np.random.default_rng(len(kind) * 1000 + 29)
+    x16 = _chosen_logits(kind, rng)
+    x = x16.astype(np.float32)
+    w[:, 0] = torch.from_numpy(x16).cuda()
+    lo = torch.empty(V, dtype=torch.float32, device="cuda")
+    params = [(0.8, 0, 0.9), (1.0, 0, 0.5), (3.0, 0, 0.99), (0.7, 300, 1.0), (1.0, 3000, 0.9), (0.9, V, 0.8),
+              (1.5, 129, 0.95), (0.5, 0, 0.3)]
+    paths = set()
+    exempt = 0
+    for temperature, top_k, top_p in params:
+        paths.add(bool(_u_decides(x, temperature, top_k, top_p)))
+        for d in range(3):
+            seed, pos = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**31 - 1))
+            got = int(ext.lm_head_sample(h, w, temperature, top_k, top_p, seed, pos, lo).item())
+            assert np.array_equal(lo.cpu().numpy(), x, equal_nan=True)
+            want, info = sp.sample(x, temperature, top_k, top_p, seed, pos, details=True)
+            if got != want and _exempt(info):
+                exempt += 1
+                continue
+            assert got == want, f"{kind} T {temperature} k {top_k} p {top_p} seed {seed} pos {pos}: " \
+                                f"device {got}, oracle {want} ({info})"
+    assert ext.last_error() == 0
+    assert exempt <= 2
+    if kind in ("normal", "grid", "special"):
+        assert paths == {True, False}
+    if kind in ("cluster", "flat"):
+        assert False in paths
 
 
 def test_sampling_refused_while_tracing(ext, lm_e0):
@@ -283,11 +341,13 @@ def _prefilled(full, ext):
     return st
 
 
-# (0.8, 50, 0.95), (0.7, 3, 0.5), (1.0, 128, 1.0) and temperature alone are drawn inside the
-# decode kernel; top-p alone and top_k > 128 by the sampler kernel after each decode step
+# every form is drawn inside the decode kernel: (0.8, 50, 0.95), (0.7, 3, 0.5), (1.0, 128, 1.0) by
+# the top-k build, temperature alone by its own build, top-p alone and top_k > 128 by the
+# split-capable build
 @pytest.mark.parametrize("temperature,top_k,top_p,seed", [(0.8, 50, 0.95, 1234), (1.5, 0, 1.0, 99),
                                                           (1.0, 0, 0.7, 2**63 + 5), (0.7, 3, 0.5, 5),
-                                                          (1.0, 128, 1.0, 8), (0.9, 200, 1.0, 7)])
+                                                          (1.0, 128, 1.0, 8), (0.9, 200, 1.0, 7),
+                                                          (1.1, 5000, 0.9, 13)])
 def test_generate_sampled_matches_replay(ext, full, temperature, top_k, top_p, seed):
     """24 sampled steps after a 16-id prompt; the same ids teacher forced give every step's
     logits bit for bit, from which the sampler (device, and oracle up to exemptions) picks
@@ -313,11 +373,12 @@ def test_generate_sampled_matches_replay(ext, full, temperature, top_k, top_p, s
     assert ids != [int(np.argmax(lo[s])) for s in range(n)]
 
 
-@pytest.mark.parametrize("top_k,top_p", [(50, 0.95), (0, 1.0)])
+@pytest.mark.parametrize("top_k,top_p", [(50, 0.95), (0, 1.0), (0, 0.95)])
 def test_generate_sampled_long_replay_at_bench_shape(ext, full, top_k, top_p):
     """The sampled benchmarks' shape: a 1000-id prompt prefilled, then 256 steps (positions
     999..1254) drawn inside the decode kernel with temperature 0.8 and top-k 50, top-p 0.95 (the
-    top-k build) or nothing else (the temperature-only build). The same ids teacher forced give
+    top-k build), nothing else (the temperature-only build) or top-p 0.95 alone (the
+    split-capable build). The same ids teacher forced give
     every step's logits, from which the sampler kernel picks exactly the run's ids; the K/V caches
     of the two runs are identical."""
     temperature, seed, n = 0.8, 7, 256
@@ -360,7 +421,7 @@ def test_generate_sampled_seeds(ext, full):
     assert runs[0] != runs[2]
 
 
-@pytest.mark.parametrize("top_k,top_p", [(0, 1.0), (40, 0.9)])
+@pytest.mark.parametrize("top_k,top_p", [(0, 1.0), (40, 0.9), (0, 0.9), (300, 1.0)])
 def test_generate_sampled_ends_at_eos(ext, full, top_k, top_p):
     start, n = len(PROMPT) - 1, 24
     ids, _ = _prefilled(full, ext).sampled(ext, PROMPT[-1], n, start, 1.2, top_k, top_p, 31)
@@ -430,7 +491,7 @@ def test_sampling_c_abi(ext, full):
     assert lib.qwen_sample(x.data_ptr(), V, 1.0, -1, 1.0, 0, 0, out.data_ptr(), stream) == 1     # top_k < 0
     assert lib.qwen_sample(None, V, 1.0, 0, 1.0, 0, 0, out.data_ptr(), stream) == 1
     start, n = len(PROMPT) - 1, 12
-    for t_, k_, p_ in [(0.9, 0, 1.0), (0.9, 40, 0.9)]:
+    for t_, k_, p_ in [(0.9, 0, 1.0), (0.9, 40, 0.9), (0.9, 0, 0.9)]:
         a = _prefilled(full, ext)
         ref, _ = a.sampled(ext, PROMPT[-1], n, start, t_, k_, p_, 123)
         b = _prefilled(full, ext)

@@ -250,37 +250,27 @@ def _sampled_ref(hw, prompt, n, eos=None, **kw):
     return out
 
 
-def test_generate_ids_sampled_chunks_and_eos(qa_cpu, small_hw):
-    """temperature > 0 goes to generate_sampled; with an eos id and top-p alone (a decode
-    launch and a sampler launch per step) the Decoder enqueues SAMPLED_CHUNK steps at a
-    time, continues from the last id and position, and stops after the eos; the draws depend
-    on the position only, so chunking changes nothing. With top-k the decode kernel draws
-    the tokens and stops at the eos itself: one call."""
+def test_generate_ids_sampled_one_call_and_eos(qa_cpu, small_hw):
+    """temperature > 0 goes to generate_sampled as one call for every parameter set (top-p
+    alone, top-k with and without top-p, a top-k above the single-kernel fast path,
+    temperature alone): the device draws the tokens and stops after the eos, which ends the
+    list; the position advances by the tokens drawn. Greedy settings take the greedy path."""
     mod, stub = qa_cpu
-    mod.SAMPLED_CHUNK = 3
-    kw = dict(temperature=1.3, top_k=0, top_p=0.9, seed=77)
     prompt = [3, 1, 4, 1, 5]
-    ref = _sampled_ref(small_hw, prompt, 10, **kw)
     dec = mod.Decoder(weights=_weights(mod), verbose=False)
-    assert dec.generate_ids(prompt, 10, **kw) == ref
-    assert stub.calls[-1] == ("generate_sampled", 5, 4, 10, -1)  # no eos: one launch sequence
-    k = next(i for i in range(4, 10) if ref[i] not in ref[:i])
-    stub.oracle.reset()
-    stub.calls.clear()
-    out = dec.generate_ids(prompt, 10, eos_token_id=ref[k], **kw)
-    assert out == ref[:k + 1]
-    assert dec.position == len(prompt) - 1 + k + 1
-    sampled = [c for c in stub.calls if c[0] == "generate_sampled"]
-    assert [c[2] for c in sampled] == list(range(4, 4 + k + 1, 3))  # chunk starts
-    assert all(c[1] == (5 if i == 0 else ref[3 * i - 1]) for i, c in enumerate(sampled))
-    # top-k (and temperature alone) in one call, eos included
-    for kk in (dict(temperature=1.3, top_k=20, top_p=0.9, seed=77), dict(temperature=1.3, top_k=0, top_p=1.0, seed=5)):
-        ref2 = _sampled_ref(small_hw, prompt, 10, **kk)
-        k2 = next(i for i in range(4, 10) if ref2[i] not in ref2[:i])
+    for kw in (dict(temperature=1.3, top_k=0, top_p=0.9, seed=77), dict(temperature=1.3, top_k=20, top_p=0.9, seed=77),
+               dict(temperature=1.1, top_k=300, top_p=1.0, seed=3), dict(temperature=1.3, top_k=0, top_p=1.0, seed=5)):
+        ref = _sampled_ref(small_hw, prompt, 10, **kw)
         stub.oracle.reset()
         stub.calls.clear()
-        assert dec.generate_ids(prompt, 10, eos_token_id=ref2[k2], **kk) == ref2[:k2 + 1]
-        assert [c for c in stub.calls if c[0] == "generate_sampled"] == [("generate_sampled", 5, 4, 10, ref2[k2])]
+        assert dec.generate_ids(prompt, 10, **kw) == ref
+        assert stub.calls[-1] == ("generate_sampled", 5, 4, 10, -1)
+        k = next(i for i in range(4, 10) if ref[i] not in ref[:i])
+        stub.oracle.reset()
+        stub.calls.clear()
+        assert dec.generate_ids(prompt, 10, eos_token_id=ref[k], **kw) == ref[:k + 1]
+        assert dec.position == len(prompt) - 1 + k + 1
+        assert [c for c in stub.calls if c[0] == "generate_sampled"] == [("generate_sampled", 5, 4, 10, ref[k])]
     # greedy settings take the greedy path
     stub.calls.clear()
     stub.oracle.reset()
