@@ -418,13 +418,14 @@ constexpr long PF_XN = PF_IM + (long)MAX_SEQ_LIMIT * INTER * 2;
 constexpr long PF_SSQ = PF_XN + (long)MAX_SEQ_LIMIT * HIDDEN * 2;
 constexpr long PF_BAR = PF_SSQ + (long)MAX_SEQ_LIMIT * 32 * 4;
 constexpr int PF_NTS = 1 + 1 + 5 * MAX_LAYERS;  // launch start, then every grid barrier
-constexpr long PF_BAR_LINES = 4096;              // barrier counters and flags, one 128-byte line each
+constexpr long PF_BAR_LINES = 4096;              // barrier words: 8 XCDs x 64 arrivals, then 8 leaders
 constexpr long PF_ACNT = PF_BAR + PF_BAR_LINES;
 constexpr long PF_BAR_BYTES = PF_BAR_LINES + 4L * pf::MAX_QB * NKV;
 constexpr long PF_TS = PF_BAR + PF_BAR_BYTES;
 constexpr long PF_PART = (PF_TS + 8L * ((PF_NTS + 31) / 32 * 32) + 255) / 256 * 256;
 constexpr long PF_BYTES = PF_PART + 4L * pf::MAX_PSLOTS * NKV * pf::PART_FLOATS;
 static_assert(PF_BAR_BYTES % 4 == 0 && PF_PART % 256 == 0, "prefill workspace alignment");
+static_assert(4L * (64 + 1) * NXCD <= PF_BAR_LINES, "the barrier words fit their lines");
 
 // The attention work of a prefill of n positions from position start: query block b (positions
 // start + 32 b ..) reads key blocks 0 .. nkb(b) - 1 (64 keys each, causal), in chunks of
