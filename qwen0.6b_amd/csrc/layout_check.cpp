@@ -456,24 +456,6 @@ int main() {
           CHECK(distinct(u, 16), "gemm operand read: bank units repeat (base %d ks %d group %d)", base, ks, g);
           CHECK(!distinct(un, 16), "the natural chunk order would not conflict (the check would be vacuous)");
         }
-    // gate/up ring: tile rows of 64 bytes, one 32-wide K step per stage; a read takes rows
-    // base + (lane % 16) and logical chunk c = lane / 16 at position c ^ pf_swz4(row)
-    for (int base = 0; base < 320; base += 16)
-      for (int g = 0; g < 4; ++g) {
-        int u[16], un[16];
-        for (int fr = 0; fr < 16; ++fr) {
-          const int row = base + fr;
-          u[fr] = ((row * 64 + 16 * (g ^ pf_swz4(row))) / 16) % 16;
-          un[fr] = ((row * 64 + 16 * g) / 16) % 16;
-        }
-        CHECK(distinct(u, 16), "gate/up operand read: bank units repeat (base %d group %d)", base, g);
-        CHECK(!distinct(un, 16), "the natural chunk order would not conflict (the check would be vacuous)");
-      }
-    for (int r = 0; r < 16; ++r) {
-      int p4[4];
-      for (int q = 0; q < 4; ++q) p4[q] = q ^ pf_swz4(r);
-      CHECK(distinct(p4, 4), "64-byte row permutation is a bijection (row %d)", r);
-    }
     for (int r = 0; r < 16; ++r) {
       int p8[8], pk[16], pv[16];
       for (int q = 0; q < 8; ++q) p8[q] = q ^ pf_swz8(r);

@@ -309,8 +309,6 @@ QL_HD unsigned tag_dist(unsigned epoch, int round) { return (epoch << 8) | (unsi
 // reads of V, 4.45x slower. layout_check verifies that property for these permutations.
 // GEMM ring rows (128 bytes, 8 chunks): logical chunk q of tile row r at position q ^ pf_swz8(r)
 QL_HD int pf_swz8(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
-// gate/up ring rows (64 bytes, 4 chunks): logical chunk q of tile row r at position q ^ pf_swz4(r)
-QL_HD int pf_swz4(int r) { return (r >> 2) & 3; }
 // attention key rows (256 bytes, 16 chunks): chunk q of key row r at position pf_kpos(q, r) for
 // K, pf_vpos(q, r) for V (each its own inverse: the DMA lane at position p loads source chunk
 // pf_kpos(p, r))
