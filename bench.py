@@ -44,13 +44,14 @@ def algorithmic_bytes(start, n):
 
 
 TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "qwen_decode_kernel.ctx2048.hbm_counters.md")
+PREFILL_TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "qwen_prefill_kernel.prompt1920.kernel_trace.md")
 
 
-def measured_traffic():
-    """HBM bytes per launch of this workload from the committed rocprofv3 counter summary
+def measured_traffic(summary=TRAFFIC_SUMMARY):
+    """HBM bytes per launch of a workload from its committed rocprofv3 counter summary
     (FETCH_SIZE + WRITE_SIZE, each scaled against a copy kernel of known size), or None."""
     try:
-        with open(TRAFFIC_SUMMARY) as f:
+        with open(summary) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":")[1])
@@ -354,7 +355,7 @@ def run_prefill(args):
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic: seeded N(0,0.02) fp16 weights (norms 1.0)",
         "config": {"workload": "prefill", "prompt": PREFILL, "layers": 28},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "traffic": measured_traffic(PREFILL_TRAFFIC_SUMMARY),
                      "kernel": "pf::qwen_prefill_kernel", "flops_per_launch": flops, "kernel_ms": round(ms, 4)},
         "phases_us_per_layer": phases,
         "cpu_baseline": None,
