@@ -109,8 +109,6 @@ QL_HD int stage_lines(int st, int ctx, int s) {
     default: return 0;
   }
 }
-// stages of a layer in execution order; MLP mode runs GU..DSUM only
-QL_HD int first_stage(int mode) { return mode == MODE_MLP ? S_GU : S_QKV; }
 
 // ---- loader streams ------------------------------------------------------------------
 // The ring lines of a layer come from 10 streams, in this order: 0 input norm (2
