@@ -228,7 +228,10 @@ def _prefill(ext, run, ids, start):
     assert ext.last_error() == 0
 
 
-@pytest.mark.parametrize("n", [16, 128, 1920])
+# prompt lengths: the n - 1 prefilled positions sit on both sides of every tiling boundary
+# (a single position; 32 and 64 positions, the attention query and key blocks; 128, a GEMM
+# tile's rows; 1024, an attention key chunk) and at the benchmark's 1919
+@pytest.mark.parametrize("n", [2, 16, 33, 34, 65, 66, 128, 129, 130, 1025, 1026, 1920])
 def test_batched_prefill_matches_oracle(ext, rn, n):
     """Batched (MFMA) prefill of an n-id prompt on the rn model (non-unit norms, untied
     lm_head), 28 layers: the K/V cache of all n - 1 prefilled positions and the prefill's
