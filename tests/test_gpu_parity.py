@@ -72,9 +72,9 @@ def rn(qa):
 class Run:
     """Device state for one teacher-forced engine run."""
 
-    def __init__(self, w, packed, layers):
-        self.w, self.packed, self.L = w, packed, layers
-        self.kc = torch.zeros(layers, 8, MAX_SEQ, 128, dtype=torch.float16, device="cuda")
+    def __init__(self, w, packed, layers, max_seq=MAX_SEQ):
+        self.w, self.packed, self.L, self.ms = w, packed, layers, max_seq
+        self.kc = torch.zeros(layers, 8, max_seq, 128, dtype=torch.float16, device="cuda")
         self.vc = torch.zeros_like(self.kc)
         self.hidden = torch.empty(1024, dtype=torch.float16, device="cuda")
         self.norm_out = torch.empty(1024, dtype=torch.float32, device="cuda")
@@ -87,7 +87,7 @@ class Run:
         w = self.w
         out = ext.generate_ex(ids[0], n, f, w["embed_weight"], self.packed, w["final_norm_weight"],
                               w["lm_head_weight"], w["cos_table"], w["sin_table"], self.kc, self.vc, self.hidden,
-                              self.norm_out, lo, hs, self.L, start, MAX_SEQ, SCALE)
+                              self.norm_out, lo, hs, self.L, start, self.ms, SCALE)
         torch.cuda.synchronize()
         assert ext.last_error() == 0
         return out.cpu().tolist(), (lo.cpu() if logits else None), (hs.cpu() if hidden else None)
@@ -223,7 +223,7 @@ def _prefill(ext, run, ids, start):
     w = run.w
     f = torch.tensor(ids, dtype=torch.int32, device="cuda")
     ext.prefill(f, w["embed_weight"], run.packed, w["cos_table"], w["sin_table"], run.kc, run.vc, run.hidden,
-                run.L, start, MAX_SEQ, SCALE)
+                run.L, start, run.ms, SCALE)
     torch.cuda.synchronize()
     assert ext.last_error() == 0
 
@@ -258,6 +258,30 @@ def test_batched_prefill_matches_oracle(ext, rn, n):
     assert dh0 <= TOL_HIDDEN and dh <= TOL_HIDDEN and dl <= TOL_LOGITS
     if gap >= GAP_EXEMPT:
         assert toks[0] == ref["tokens"][0]
+
+
+def test_short_cache_max_seq_512(ext, rn):
+    """A cache of max_seq_len 512 (K and V each [28, 8, 512, 128]): every cache address the
+    prefill and decode kernels form uses the call's max_seq_len. A 399-id prefill, then 112
+    teacher-forced decode steps at positions 399..510, on the rn model: the K/V cache of all
+    511 positions, every step's logits and hidden state, and its greedy token (near-ties
+    exempt) against one oracle forward."""
+    hw, w, packed = rn
+    ids = qw.synthetic_prompt(511, seed=77)
+    oracle = orc.Oracle(hw)
+    ref = oracle.forward(ids, logits_at=list(range(399, 511)))
+    run = Run(w, packed, 28, max_seq=512)
+    _prefill(ext, run, ids[:399], 0)
+    toks, logits, hidden = run.forced(ext, ids[399:], 399)
+    dk = float((run.kc[:, :, :511].float().cpu() - oracle.k_cache[:, :, :511]).abs().max())
+    dv = float((run.vc[:, :, :511].float().cpu() - oracle.v_cache[:, :, :511]).abs().max())
+    dl = float((logits - ref["logits"]).abs().max())
+    dh = float((hidden - ref["hidden"][399:]).abs().max())
+    print(f"max_seq 512: K {dk:.3e} V {dv:.3e} logits {dl:.3e} hidden {dh:.3e}")
+    assert dk < 2e-2 and dv < 2e-2 and dl <= TOL_LOGITS and dh <= TOL_HIDDEN
+    for i, tok in enumerate(ref["tokens"]):
+        if orc.top2_gap(ref["logits"][i]) >= GAP_EXEMPT:
+            assert toks[i] == tok, f"step {i}: {toks[i]} != {tok}"
 
 
 @pytest.mark.parametrize("n,cuts", [(200, [77]), (1300, [77, 900]), (2047, [1500, 2040])])
