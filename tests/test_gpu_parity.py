@@ -491,6 +491,37 @@ def test_long_context_two_layers(ext, full, qa):
     assert float((kc - oracle.k_cache[:, :, :MAX_SEQ]).abs().max()) < 2e-2
 
 
+@pytest.mark.parametrize("layers", [1, 2])
+def test_batched_prefill_few_layers(ext, rn, qa, layers):
+    """The batched prefill with fewer layers than the model (num_layers = 1 or 2 of the rn
+    model's, as a caller may pass): the last layer's down phase writes no next norm input, so
+    its residual is what the hidden state and the decode step that follows read. A 300-id
+    prompt (299 positions prefilled), then the decode step of the last id: K/V cache, the
+    prefill's hidden state, the step's logits and hidden state against the oracle of the same
+    truncated model."""
+    hw_rn, _, _ = rn
+    hw = qw.HostWeights(shape=qw.QwenShape(layers=layers), embed=hw_rn.embed, layers=hw_rn.layers[:layers],
+                        final_norm=hw_rn.final_norm, cos=hw_rn.cos, sin=hw_rn.sin, lm_head=hw_rn.lm_head)
+    w = qw.device_weights(hw, "cuda")
+    packed = qa._pack_layer_weights(w["layer_weights"])
+    n = 300
+    ids = qw.synthetic_prompt(n, seed=90 + layers)
+    oracle = orc.Oracle(hw)
+    ref = oracle.forward(ids, logits_at=[n - 1])
+    run = Run(w, packed, layers)
+    _prefill(ext, run, ids[:-1], 0)
+    dh0 = float((run.hidden.float().cpu() - ref["hidden"][n - 2]).abs().max())
+    dk = float((run.kc[:, :, : n - 1].float().cpu() - oracle.k_cache[:, :, : n - 1]).abs().max())
+    dv = float((run.vc[:, :, : n - 1].float().cpu() - oracle.v_cache[:, :, : n - 1]).abs().max())
+    toks, logits, hidden = run.forced(ext, ids[-1:], n - 1)
+    dl = float((logits[0] - ref["logits"][0]).abs().max())
+    dh = float((hidden[0] - ref["hidden"][n - 1]).abs().max())
+    print(f"prefill {layers} layer(s): K {dk:.3e} V {dv:.3e} hidden(prefill) {dh0:.3e}; logits {dl:.3e} hidden {dh:.3e}")
+    assert dk < 2e-2 and dv < 2e-2 and dh0 <= TOL_HIDDEN and dh <= TOL_HIDDEN and dl <= TOL_LOGITS
+    if orc.top2_gap(ref["logits"][0]) >= GAP_EXEMPT:
+        assert toks[0] == ref["tokens"][0]
+
+
 def test_decode_is_deterministic_and_matches_generate(ext, full, qa):
     """decode() (one step per launch) and generate_ex give bit-identical logits,
     and two identical runs are bit-identical."""
